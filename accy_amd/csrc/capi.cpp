@@ -1,0 +1,339 @@
+// C ABI of the gfx950 target (include/accy_hip.h): a 64-entry handle table with generations, as the
+// reference session keeps (src/tensor/session/session.zig:99-246), over HIP executors.
+#include "../../include/accy_hip.h"
+
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <new>
+#include <string>
+
+#include "plan.hpp"
+#include "runtime.hpp"
+#include "wire.hpp"
+
+using namespace accy;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Entry {
+  bool live = false;
+  uint32_t generation = 0;
+  std::unique_ptr<Executor> exec;
+  // Descriptor storage: names and extents per input, then per output.
+  std::vector<std::vector<std::string>> names;
+  std::vector<std::vector<const char*>> name_ptrs;
+  std::vector<std::vector<int64_t>> extents;
+  std::vector<std::string> labels, klasses;
+};
+
+std::mutex g_mu;
+Entry g_entries[ACCY_HIP_MAX_PROGRAMS];
+
+int fail_with(int status, const std::string& msg) {
+  g_last_error = msg;
+  return status;
+}
+
+int status_of(const Error& e) {
+  switch (e.code) {
+    case Err::UnsupportedVersion: return ACCY_HIP_UNSUPPORTED_VERSION;
+    case Err::Unsupported: return ACCY_HIP_COMPILE_FAILED;
+    default: return ACCY_HIP_INVALID_PROGRAM;
+  }
+}
+
+Entry* lookup(accy_hip_handle h) {
+  if (h.index >= ACCY_HIP_MAX_PROGRAMS) return nullptr;
+  Entry& e = g_entries[h.index];
+  if (!e.live || e.generation != h.generation) return nullptr;
+  return &e;
+}
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    return f();
+  } catch (const HipFailure& e) {
+    return fail_with(e.status, e.what());
+  } catch (const Error& e) {
+    return fail_with(status_of(e), e.what());
+  } catch (const std::bad_alloc&) {
+    return fail_with(ACCY_HIP_OUT_OF_MEMORY, "out of memory");
+  } catch (const std::exception& e) {
+    return fail_with(ACCY_HIP_COMPILE_FAILED, e.what());
+  }
+}
+
+Program decode_program(const uint8_t* wire, size_t len) {
+  if (!wire && len) throw Error(Err::InvalidArtifact, "null wire bytes");
+  return wire::decode(wire, len);
+}
+
+void fill_descriptors(Entry& e) {
+  const Program& p = e.exec->program();
+  e.names.clear();
+  e.name_ptrs.clear();
+  e.extents.clear();
+  auto add = [&](uint32_t vid) {
+    const Type& t = p.type(vid);
+    std::vector<std::string> n;
+    std::vector<int64_t> x;
+    for (const Dim& d : t.dims) {
+      n.push_back(d.name);
+      x.push_back(d.extent);
+    }
+    e.names.push_back(std::move(n));
+    e.extents.push_back(std::move(x));
+  };
+  for (uint32_t v : p.params) add(v);
+  for (uint32_t v : p.outputs) add(v);
+  for (auto& n : e.names) {
+    std::vector<const char*> ptrs;
+    for (auto& s : n) ptrs.push_back(s.c_str());
+    e.name_ptrs.push_back(std::move(ptrs));
+  }
+  e.labels.clear();
+  e.klasses.clear();
+  for (const auto& t : e.exec->timings()) {
+    e.labels.push_back(t.label);
+    e.klasses.push_back(t.klass);
+  }
+}
+
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+  if (!an || !bn) return false;
+  auto x = (const uint8_t*)a, y = (const uint8_t*)b;
+  return x < y + bn && y < x + an;
+}
+
+}  // namespace
+
+extern "C" {
+
+int accy_hip_compile(const uint8_t* wire_bytes, size_t wire_len, accy_hip_handle* out) {
+  return guarded([&]() -> int {
+    if (!out) return fail_with(ACCY_HIP_INVALID_BUFFER, "null handle pointer");
+    uint32_t index = ACCY_HIP_MAX_PROGRAMS;
+    {
+      std::lock_guard<std::mutex> lock(g_mu);
+      for (uint32_t i = 0; i < ACCY_HIP_MAX_PROGRAMS; ++i)
+        if (!g_entries[i].live) {
+          index = i;
+          break;
+        }
+    }
+    if (index == ACCY_HIP_MAX_PROGRAMS) return fail_with(ACCY_HIP_TOO_MANY_PROGRAMS, "all 64 slots hold programs");
+    Program prog;
+    try {
+      prog = decode_program(wire_bytes, wire_len);
+    } catch (const Error& e) {
+      return fail_with(e.code == Err::UnsupportedVersion ? ACCY_HIP_UNSUPPORTED_VERSION : ACCY_HIP_INVALID_PROGRAM,
+                       e.what());
+    }
+    Plan plan;
+    try {
+      plan = lower(prog);
+    } catch (const Error& e) {
+      return fail_with(ACCY_HIP_COMPILE_FAILED, e.what());
+    }
+    auto exec = std::make_unique<Executor>(std::move(prog), std::move(plan));
+    std::lock_guard<std::mutex> lock(g_mu);
+    Entry* e = &g_entries[index];
+    if (e->live) {  // taken by another thread meanwhile
+      index = ACCY_HIP_MAX_PROGRAMS;
+      for (uint32_t i = 0; i < ACCY_HIP_MAX_PROGRAMS; ++i)
+        if (!g_entries[i].live) {
+          index = i;
+          break;
+        }
+      if (index == ACCY_HIP_MAX_PROGRAMS) return fail_with(ACCY_HIP_TOO_MANY_PROGRAMS, "all 64 slots hold programs");
+      e = &g_entries[index];
+    }
+    e->live = true;
+    e->exec = std::move(exec);
+    fill_descriptors(*e);
+    out->index = index;
+    out->generation = e->generation;
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_counts(accy_hip_handle h, size_t* n_inputs, size_t* n_outputs) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  Entry* e = lookup(h);
+  if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+  if (n_inputs) *n_inputs = e->exec->program().params.size();
+  if (n_outputs) *n_outputs = e->exec->program().outputs.size();
+  return ACCY_HIP_OK;
+}
+
+int accy_hip_describe(accy_hip_handle h, int which, size_t index, accy_hip_descriptor* out) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  Entry* e = lookup(h);
+  if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+  const Program& p = e->exec->program();
+  size_t n = which == 0 ? p.params.size() : p.outputs.size();
+  if (index >= n || !out) return fail_with(ACCY_HIP_INVALID_BUFFER, "descriptor index out of range");
+  size_t slot = which == 0 ? index : p.params.size() + index;
+  const Type& t = p.type(which == 0 ? p.params[index] : p.outputs[index]);
+  out->dtype = (uint32_t)t.dtype;
+  out->rank = (uint32_t)t.rank();
+  out->names = e->name_ptrs[slot].data();
+  out->extents = e->extents[slot].data();
+  out->byte_size = t.bytes();
+  out->alignment = (uint32_t)dtype_size(t.dtype);
+  return ACCY_HIP_OK;
+}
+
+int accy_hip_invoke(accy_hip_handle h, const void* const* inputs, const size_t* input_lens, size_t n_inputs,
+                    void* const* outputs, const size_t* output_lens, size_t n_outputs) {
+  Executor* ex;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    Entry* e = lookup(h);
+    if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+    ex = e->exec.get();
+  }
+  return guarded([&]() -> int {
+    if (n_inputs && (!inputs || !input_lens)) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
+    if (n_outputs && (!outputs || !output_lens)) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
+    // session.zig:173-179: an output may share no bytes with an input or another output.
+    for (size_t o = 0; o < n_outputs; ++o) {
+      for (size_t i = 0; i < n_inputs; ++i)
+        if (overlaps(outputs[o], output_lens[o], inputs[i], input_lens[i]))
+          return fail_with(ACCY_HIP_INVALID_BUFFER, "output overlaps an input");
+      for (size_t j = 0; j < o; ++j)
+        if (overlaps(outputs[o], output_lens[o], outputs[j], output_lens[j]))
+          return fail_with(ACCY_HIP_INVALID_BUFFER, "outputs overlap");
+    }
+    ex->invoke_host(inputs, input_lens, n_inputs, outputs, output_lens, n_outputs);
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t n_inputs, void* const* outputs,
+                           size_t n_outputs, void* stream) {
+  Executor* ex;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    Entry* e = lookup(h);
+    if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+    ex = e->exec.get();
+  }
+  return guarded([&]() -> int {
+    if (n_inputs && !inputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
+    if (n_outputs && !outputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
+    ex->invoke_device(inputs, n_inputs, outputs, n_outputs, (hipStream_t)stream);
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_release(accy_hip_handle h) {
+  std::unique_ptr<Executor> dead;
+  {
+    std::lock_guard<std::mutex> lock(g_mu);
+    Entry* e = lookup(h);
+    if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+    dead = std::move(e->exec);
+    uint32_t gen = e->generation + 1;
+    *e = Entry();
+    e->generation = gen;
+  }
+  return ACCY_HIP_OK;
+}
+
+int accy_hip_run(const uint8_t* wire_bytes, size_t wire_len, const void* const* inputs, const size_t* input_lens,
+                 size_t n_inputs, void* const* outputs, const size_t* output_lens, size_t n_outputs) {
+  accy_hip_handle h;
+  int s = accy_hip_compile(wire_bytes, wire_len, &h);
+  if (s != ACCY_HIP_OK) return s;
+  s = accy_hip_invoke(h, inputs, input_lens, n_inputs, outputs, output_lens, n_outputs);
+  std::string err = g_last_error;
+  accy_hip_release(h);
+  g_last_error = err;
+  return s;
+}
+
+const char* accy_hip_last_error(void) { return g_last_error.c_str(); }
+
+int accy_hip_set_profiling(accy_hip_handle h, int enable) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  Entry* e = lookup(h);
+  if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+  return guarded([&]() -> int {
+    e->exec->set_profiling(enable != 0);
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_kernel_count(accy_hip_handle h, size_t* n) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  Entry* e = lookup(h);
+  if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+  if (n) *n = e->exec->timings().size();
+  return ACCY_HIP_OK;
+}
+
+int accy_hip_kernel_info(accy_hip_handle h, size_t index, accy_hip_kernel_stats* out) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  Entry* e = lookup(h);
+  if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+  const auto& t = e->exec->timings();
+  if (index >= t.size() || !out) return fail_with(ACCY_HIP_INVALID_BUFFER, "kernel index out of range");
+  out->label = e->labels[index].c_str();
+  out->klass = e->klasses[index].c_str();
+  out->algorithmic_bytes = t[index].algorithmic_bytes;
+  out->algorithmic_flops = t[index].algorithmic_flops;
+  out->last_ms = t[index].last_ms;
+  return ACCY_HIP_OK;
+}
+
+int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile, char* buf, size_t cap,
+                         size_t* needed) {
+  return guarded([&]() -> int {
+    Program prog;
+    try {
+      prog = decode_program(wire_bytes, wire_len);
+    } catch (const Error& e) {
+      return fail_with(e.code == Err::UnsupportedVersion ? ACCY_HIP_UNSUPPORTED_VERSION : ACCY_HIP_INVALID_PROGRAM,
+                       e.what());
+    }
+    Plan plan = lower(prog);
+    std::string text;
+    for (const Step& st : plan.steps) {
+      if (st.type == Step::Copy) {
+        text += "// copy slot " + std::to_string(st.copy.src) + " -> " + std::to_string(st.copy.dst) + "\n";
+        continue;
+      }
+      const KernelStep& k = st.kernel;
+      text += "// " + k.label + " grid " + std::to_string(k.grid[0]) + " block " + std::to_string(k.block[0]) + "\n";
+      text += k.source;
+      if (compile) compile_kernel_source(full_kernel_source(k.source), k.name);
+    }
+    if (needed) *needed = text.size() + 1;
+    if (buf && cap) {
+      size_t n = std::min(cap - 1, text.size());
+      std::memcpy(buf, text.data(), n);
+      buf[n] = '\0';
+    }
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_device_arch(char* buf, size_t cap) {
+  return guarded([&]() -> int {
+    if (device_count() <= 0) return fail_with(ACCY_HIP_LAUNCH_FAILED, "no HIP device");
+    std::string a = device_arch();
+    if (buf && cap) {
+      size_t n = std::min(cap - 1, a.size());
+      std::memcpy(buf, a.data(), n);
+      buf[n] = '\0';
+    }
+    return ACCY_HIP_OK;
+  });
+}
+
+}  // extern "C"

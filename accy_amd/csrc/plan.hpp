@@ -1,0 +1,71 @@
+// Kernel plan: what the HIP target runs for one program. The planner (lower.cpp) decides which values
+// live in device buffers (slots) and which kernels compute them; the runtime (runtime.cpp) allocates
+// the slots, compiles each kernel source with hiprtc for gfx950 and launches the steps in order.
+//
+// This plays the role of the reference's artifact plan (slots: inputs / outputs / intermediates,
+// planned kernels, launch geometry; src/artifact/plan.zig:840-874, 2650-2688) and launch plan
+// (src/executable/plan.zig:410), restated for one HIP device.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "ir.hpp"
+
+namespace accy {
+
+struct SlotInfo {
+  enum Role : uint8_t { Input, Output, Temp, Const } role = Temp;
+  int io_index = -1;  // parameter / output position for Input and Output slots
+  uint64_t bytes = 0;
+  DType dtype = DType::f32;
+  std::string data;  // Const payload, uploaded once at compile time
+};
+
+struct KernelStep {
+  std::string source;        // complete HIP source, compiled with hiprtc
+  std::string name;          // extern "C" symbol in `source`
+  std::vector<int> args;     // slot ids passed as device pointers, in parameter order
+  uint32_t grid[3] = {1, 1, 1};
+  uint32_t block[3] = {64, 1, 1};
+  uint32_t shared_bytes = 0;
+  std::string label;         // class and root value, e.g. "row:%11"
+  std::string klass;         // "map", "row", "fold", "dot", "gemm", "attention", ...
+  double algorithmic_bytes = 0;  // HBM bytes the kernel must move (inputs read once, outputs written)
+  double algorithmic_flops = 0;  // useful floating-point work
+};
+
+struct CopyStep {
+  int src = -1, dst = -1;
+  uint64_t bytes = 0;
+};
+
+struct Step {
+  enum Type : uint8_t { Kernel, Copy } type = Kernel;
+  KernelStep kernel;
+  CopyStep copy;
+};
+
+struct Plan {
+  std::vector<SlotInfo> slots;
+  std::vector<Step> steps;
+  std::vector<int> input_slots;   // per parameter
+  std::vector<int> output_slots;  // per program output
+};
+
+struct LowerOptions {
+  bool allow_gemm = true;       // MFMA contraction kernels for f32 / f16 / bf16
+  bool allow_attention = true;  // fused QK^T -> softmax -> V
+  bool allow_row = true;        // fused row pipelines (else serial folds)
+};
+
+// Lowers a decoded program. Throws accy::Error(Unsupported) for operations the target cannot run.
+Plan lower(const Program& program, const LowerOptions& options = {});
+
+// Device source shared by every generated kernel (kernels/common.h), embedded at build time.
+extern const char* const kCommonDeviceSource;
+extern const char* const kGemmDeviceSource;
+extern const char* const kAttentionDeviceSource;
+
+}  // namespace accy

@@ -1,0 +1,222 @@
+// HIP runtime for the gfx950 target. Kernels are compiled once per distinct source with hiprtc and
+// cached for the life of the process; every executor owns its intermediate buffers and launches its
+// plan in order on one stream (default priority).
+#include "runtime.hpp"
+
+#include <hip/hiprtc.h>
+
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+namespace accy {
+
+extern const char* const kCommonDeviceSource;
+
+namespace {
+
+void check(hipError_t e, const char* what, int status = kStatusLaunchFailed) {
+  if (e == hipSuccess) return;
+  if (e == hipErrorOutOfMemory) status = kStatusOutOfMemory;
+  throw HipFailure(status, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+struct Module {
+  hipModule_t module = nullptr;
+  hipFunction_t function = nullptr;
+};
+
+std::mutex g_cache_mu;
+std::unordered_map<std::string, Module>& module_cache() {
+  static auto* c = new std::unordered_map<std::string, Module>();  // lives until process exit
+  return *c;
+}
+
+hipFunction_t load_kernel(const std::string& body, const std::string& name) {
+  std::string key = name + '\0' + body;
+  {
+    std::lock_guard<std::mutex> lock(g_cache_mu);
+    auto it = module_cache().find(key);
+    if (it != module_cache().end()) return it->second.function;
+  }
+  std::vector<char> code = compile_kernel_source(full_kernel_source(body), name);
+  Module m;
+  check(hipModuleLoadData(&m.module, code.data()), "hipModuleLoadData", kStatusCompileFailed);
+  check(hipModuleGetFunction(&m.function, m.module, name.c_str()), "hipModuleGetFunction", kStatusCompileFailed);
+  std::lock_guard<std::mutex> lock(g_cache_mu);
+  module_cache()[key] = m;
+  return m.function;
+}
+
+}  // namespace
+
+std::string full_kernel_source(const std::string& body) {
+  return std::string(kCommonDeviceSource) + "\n" + body;
+}
+
+std::vector<char> compile_kernel_source(const std::string& source, const std::string& name) {
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, source.c_str(), (name + ".hip").c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    throw HipFailure(kStatusCompileFailed, "hiprtcCreateProgram failed");
+  // Packed-f32 instructions stay disabled for every kernel this target builds.
+  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+                        "-Xclang", "-packed-fp32-ops"};
+  hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t n = 0;
+    hiprtcGetProgramLogSize(prog, &n);
+    std::string log(n, '\0');
+    if (n) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    throw HipFailure(kStatusCompileFailed, "hiprtc failed for " + name + ":\n" + log);
+  }
+  size_t size = 0;
+  hiprtcGetCodeSize(prog, &size);
+  std::vector<char> code(size);
+  hiprtcGetCode(prog, code.data());
+  hiprtcDestroyProgram(&prog);
+  return code;
+}
+
+int device_count() {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+std::string device_arch() {
+  int dev = 0;
+  check(hipGetDevice(&dev), "hipGetDevice");
+  hipDeviceProp_t p;
+  check(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties");
+  return p.gcnArchName;
+}
+
+Executor::Executor(Program program, Plan plan) : program_(std::move(program)), plan_(std::move(plan)) {
+  if (device_count() <= 0) throw HipFailure(kStatusCompileFailed, "no HIP device");
+  std::string arch = device_arch();
+  if (arch.rfind("gfx950", 0) != 0) throw HipFailure(kStatusCompileFailed, "device is " + arch + ", not gfx950");
+  owned_.assign(plan_.slots.size(), nullptr);
+  bound_.assign(plan_.slots.size(), nullptr);
+  try {
+    check(hipStreamCreate(&stream_), "hipStreamCreate");
+    for (size_t i = 0; i < plan_.slots.size(); ++i) {
+      const SlotInfo& s = plan_.slots[i];
+      if (s.role == SlotInfo::Input || s.role == SlotInfo::Output || s.bytes == 0) continue;
+      check(hipMalloc(&owned_[i], s.bytes), "hipMalloc");
+      if (s.role == SlotInfo::Const)
+        check(hipMemcpy(owned_[i], s.data.data(), s.bytes, hipMemcpyHostToDevice), "hipMemcpy");
+    }
+    fn_.assign(plan_.steps.size(), nullptr);
+    for (size_t i = 0; i < plan_.steps.size(); ++i) {
+      const Step& st = plan_.steps[i];
+      if (st.type != Step::Kernel) continue;
+      fn_[i] = load_kernel(st.kernel.source, st.kernel.name);
+      KernelTiming t;
+      t.label = st.kernel.label;
+      t.klass = st.kernel.klass;
+      t.algorithmic_bytes = st.kernel.algorithmic_bytes;
+      t.algorithmic_flops = st.kernel.algorithmic_flops;
+      timings_.push_back(t);
+    }
+  } catch (...) {
+    for (void* p : owned_)
+      if (p) (void)hipFree(p);
+    if (stream_) (void)hipStreamDestroy(stream_);
+    throw;
+  }
+}
+
+Executor::~Executor() {
+  if (stream_) (void)hipStreamSynchronize(stream_);
+  for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+  for (void* p : owned_)
+    if (p) (void)hipFree(p);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Executor::set_profiling(bool on) {
+  profiling_ = on;
+  if (on && events_.empty()) {
+    size_t n = 0;
+    for (const Step& st : plan_.steps)
+      if (st.type == Step::Kernel) ++n;
+    events_.resize(2 * n);
+    for (auto& e : events_) check(hipEventCreate(&e), "hipEventCreate");
+  }
+}
+
+void Executor::run_steps(hipStream_t stream) {
+  for (size_t i = 0; i < plan_.slots.size(); ++i)
+    if (plan_.slots[i].role == SlotInfo::Temp || plan_.slots[i].role == SlotInfo::Const) bound_[i] = owned_[i];
+  size_t ki = 0;
+  for (size_t i = 0; i < plan_.steps.size(); ++i) {
+    const Step& st = plan_.steps[i];
+    if (st.type == Step::Copy) {
+      check(hipMemcpyAsync(bound_[(size_t)st.copy.dst], bound_[(size_t)st.copy.src], st.copy.bytes,
+                           hipMemcpyDeviceToDevice, stream),
+            "hipMemcpyAsync");
+      continue;
+    }
+    const KernelStep& k = st.kernel;
+    std::vector<void*> ptrs(k.args.size());
+    std::vector<void*> params(k.args.size());
+    for (size_t a = 0; a < k.args.size(); ++a) {
+      ptrs[a] = bound_[(size_t)k.args[a]];
+      params[a] = &ptrs[a];
+    }
+    if (profiling_) check(hipEventRecord(events_[2 * ki], stream), "hipEventRecord");
+    check(hipModuleLaunchKernel(fn_[i], k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2],
+                                k.shared_bytes, stream, params.data(), nullptr),
+          "hipModuleLaunchKernel");
+    if (profiling_) check(hipEventRecord(events_[2 * ki + 1], stream), "hipEventRecord");
+    ++ki;
+  }
+}
+
+void Executor::invoke_device(const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs,
+                             hipStream_t stream) {
+  if (n_inputs != plan_.input_slots.size() || n_outputs != plan_.output_slots.size())
+    throw HipFailure(kStatusInvalidBuffer, "buffer count mismatch");
+  for (size_t i = 0; i < n_inputs; ++i) bound_[(size_t)plan_.input_slots[i]] = const_cast<void*>(inputs[i]);
+  for (size_t i = 0; i < n_outputs; ++i) bound_[(size_t)plan_.output_slots[i]] = outputs[i];
+  run_steps(stream);
+  if (profiling_) {
+    check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+    for (size_t k = 0; k < timings_.size(); ++k)
+      check(hipEventElapsedTime(&timings_[k].last_ms, events_[2 * k], events_[2 * k + 1]), "hipEventElapsedTime");
+  }
+}
+
+void Executor::invoke_host(const void* const* inputs, const size_t* input_lens, size_t n_inputs,
+                           void* const* outputs, const size_t* output_lens, size_t n_outputs) {
+  if (n_inputs != plan_.input_slots.size() || n_outputs != plan_.output_slots.size())
+    throw HipFailure(kStatusInvalidBuffer, "buffer count mismatch");
+  for (size_t i = 0; i < n_inputs; ++i)
+    if (input_lens[i] != plan_.slots[(size_t)plan_.input_slots[i]].bytes)
+      throw HipFailure(kStatusInvalidBuffer, "input " + std::to_string(i) + " size mismatch");
+  for (size_t i = 0; i < n_outputs; ++i)
+    if (output_lens[i] != plan_.slots[(size_t)plan_.output_slots[i]].bytes)
+      throw HipFailure(kStatusInvalidBuffer, "output " + std::to_string(i) + " size mismatch");
+  // Staging buffers for host invocations are allocated on first use and kept.
+  for (int s : plan_.input_slots)
+    if (!owned_[(size_t)s] && plan_.slots[(size_t)s].bytes) check(hipMalloc(&owned_[(size_t)s], plan_.slots[(size_t)s].bytes), "hipMalloc");
+  for (int s : plan_.output_slots)
+    if (!owned_[(size_t)s] && plan_.slots[(size_t)s].bytes) check(hipMalloc(&owned_[(size_t)s], plan_.slots[(size_t)s].bytes), "hipMalloc");
+  std::vector<const void*> din(n_inputs);
+  std::vector<void*> dout(n_outputs);
+  for (size_t i = 0; i < n_inputs; ++i) {
+    size_t s = (size_t)plan_.input_slots[i];
+    din[i] = owned_[s];
+    if (input_lens[i])
+      check(hipMemcpyAsync(owned_[s], inputs[i], input_lens[i], hipMemcpyHostToDevice, stream_), "hipMemcpyAsync");
+  }
+  for (size_t i = 0; i < n_outputs; ++i) dout[i] = owned_[(size_t)plan_.output_slots[i]];
+  invoke_device(din.data(), n_inputs, dout.data(), n_outputs, stream_);
+  for (size_t i = 0; i < n_outputs; ++i)
+    if (output_lens[i])
+      check(hipMemcpyAsync(outputs[i], dout[i], output_lens[i], hipMemcpyDeviceToHost, stream_), "hipMemcpyAsync");
+  check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
+}
+
+}  // namespace accy

@@ -1,0 +1,77 @@
+// HIP runtime for the gfx950 target: kernel compilation (hiprtc), module cache, device buffers and
+// execution of a kernel plan on one stream. This is the device layer the reference reaches through
+// its backend vtable (deps/lib/compiler/gpu/src/contract.zig:2048-2084): load_artifact,
+// allocate_buffer, write_buffer / read_buffer, launch, synchronize, destroy_object.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "ir.hpp"
+#include "plan.hpp"
+
+namespace accy {
+
+// A failure with the status number it maps to (src/tensor/session/session.zig:33-43).
+struct HipFailure : std::runtime_error {
+  int status;
+  HipFailure(int s, const std::string& m) : std::runtime_error(m), status(s) {}
+};
+
+constexpr int kStatusOk = 0, kStatusInvalidProgram = 1, kStatusUnsupportedVersion = 2, kStatusInvalidHandle = 3,
+              kStatusInvalidBuffer = 4, kStatusTooManyPrograms = 5, kStatusOutOfMemory = 6,
+              kStatusCompileFailed = 7, kStatusLaunchFailed = 8;
+
+// Compiles one generated kernel source for gfx950 with hiprtc; returns the code object.
+std::vector<char> compile_kernel_source(const std::string& source, const std::string& name);
+
+// The complete text hiprtc receives for a generated kernel: device helpers + kernel body.
+std::string full_kernel_source(const std::string& body);
+
+struct KernelTiming {
+  std::string label, klass;
+  double algorithmic_bytes = 0, algorithmic_flops = 0;
+  float last_ms = 0;
+};
+
+// A compiled program bound to device memory: the HIP counterpart of the reference's loaded fragment.
+class Executor {
+ public:
+  Executor(Program program, Plan plan);
+  ~Executor();
+  Executor(const Executor&) = delete;
+  Executor& operator=(const Executor&) = delete;
+
+  const Program& program() const { return program_; }
+  const Plan& plan() const { return plan_; }
+
+  // Host slices in, host slices out; sizes must equal the descriptors' byte sizes.
+  void invoke_host(const void* const* inputs, const size_t* input_lens, size_t n_inputs, void* const* outputs,
+                   const size_t* output_lens, size_t n_outputs);
+  // Device pointers in and out, enqueued on `stream`, no synchronisation.
+  void invoke_device(const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs,
+                     hipStream_t stream);
+
+  void set_profiling(bool on);
+  const std::vector<KernelTiming>& timings() const { return timings_; }
+
+ private:
+  void run_steps(hipStream_t stream);
+  Program program_;
+  Plan plan_;
+  std::vector<void*> owned_;     // device allocation per slot (Temp / Const; staging for Input / Output)
+  std::vector<void*> bound_;     // pointer used for each slot during a run
+  std::vector<hipFunction_t> fn_;
+  hipStream_t stream_ = nullptr;
+  bool profiling_ = false;
+  std::vector<hipEvent_t> events_;
+  std::vector<KernelTiming> timings_;
+};
+
+int device_count();
+std::string device_arch();
+
+}  // namespace accy

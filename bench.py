@@ -1,0 +1,185 @@
+"""Benchmark of the MI355X execution target on the reference's measured configurations.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2-lse]`` prints ONE JSON line.
+
+* A step is one launch of the compiled program (``Hip.launch_device``) over inputs already resident
+  in HBM, on torch's current stream; K steps are timed between two synchronisations.
+* ``value`` is the whole-job throughput of the step: algorithmic bytes (HBM-bound configs) or
+  algorithmic FLOP (MFMA / VALU-bound configs) per second, with the per-config figures of the
+  measurement plan.
+* ``roofline`` is for the dominant kernel: its algorithmic bytes or FLOP per launch divided by its
+  average duration, measured with HIP events recorded on the launch stream around that kernel.
+* ``cpu_baseline`` is the CPU oracle (the runCpu restatement, oracle/) timed on this host on a
+  bounded sample of the same workload, then scaled to the metric's unit (kind "port").
+
+The default workload is C2 (row-wise logsumexp, x f32[32768, 8192]), the configuration the metric
+is quoted on that fits one GPU. Other configs are parity cases; ``--config`` measures them too.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from accy_amd import hip  # noqa: E402
+from accy_amd import tensor as T  # noqa: E402
+from accy_amd import workloads as W  # noqa: E402
+
+METRIC = "GB/s & TFLOP/s per config as % of MI355X roofline; speedup vs runCpu"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0, "f16": 2500.0}
+VALU_PEAK_TFLOPS = 157.3
+
+
+def config_table():
+    """Per config: program, inputs, algorithmic work, unit, bound, oracle sample."""
+    return {
+        "c1-tone": dict(
+            make=lambda: (W.tone_program(8192, 16384), W.tone_inputs(8192, 16384, seed=1)),
+            dtype="f32", unit="GFLOP/s", bound="valu", work=4.0 * 8192 * 16384, peak=VALU_PEAK_TFLOPS * 1000,
+            sample=lambda: (W.tone_program(256, 16384), W.tone_inputs(256, 16384, seed=1), 4.0 * 256 * 16384),
+            sample_desc="256 of 8192 guesses x 16384 points", workload=dict(guesses=8192, points=16384)),
+        "c2-lse": dict(
+            make=lambda: (W.logsumexp_program(32768, 8192), W.logsumexp_inputs(32768, 8192, seed=2)),
+            dtype="f32", unit="GB/s", bound="hbm", work=32768 * 8192 * 4 + 32768 * 4, peak=HBM_PEAK_GBS,
+            sample=lambda: (W.logsumexp_program(4096, 8192), W.logsumexp_inputs(4096, 8192, seed=2),
+                            4096 * 8192 * 4 + 4096 * 4),
+            sample_desc="4096 of 32768 rows x 8192 features", workload=dict(rows=32768, features=8192)),
+        "c3-gemm-f32": dict(
+            make=lambda: (W.gemm_program(8192, 8192, 8192, "f32"), W.gemm_inputs(8192, 8192, 8192, "f32")),
+            dtype="f32", unit="TFLOP/s", bound="mfma", work=2.0 * 8192 ** 3, peak=MFMA_PEAK_TFLOPS["f32"],
+            sample=lambda: (W.gemm_program(16, 8192, 8192, "f32"), W.gemm_inputs(16, 8192, 8192, "f32"),
+                            2.0 * 16 * 8192 * 8192),
+            sample_desc="16 of 8192 rows of A", workload=dict(m=8192, k=8192, n=8192)),
+        "c3-gemm-bf16": dict(
+            make=lambda: (W.gemm_program(8192, 8192, 8192, "bf16"), W.gemm_inputs(8192, 8192, 8192, "bf16")),
+            dtype="bf16", unit="TFLOP/s", bound="mfma", work=2.0 * 8192 ** 3, peak=MFMA_PEAK_TFLOPS["bf16"],
+            sample=lambda: (W.gemm_program(16, 8192, 8192, "bf16"), W.gemm_inputs(16, 8192, 8192, "bf16"),
+                            2.0 * 16 * 8192 * 8192),
+            sample_desc="16 of 8192 rows of A", workload=dict(m=8192, k=8192, n=8192)),
+        "c4-attention": dict(
+            make=lambda: (W.attention_program(32, 4096, 128, "f16"), W.attention_inputs(32, 4096, 128, "f16")),
+            dtype="f16", unit="TFLOP/s", bound="mfma", work=4.0 * 32 * 4096 * 4096 * 128,
+            peak=MFMA_PEAK_TFLOPS["f16"],
+            sample=lambda: (W.attention_program(1, 1024, 128, "f16"), W.attention_inputs(1, 1024, 128, "f16"),
+                            4.0 * 1 * 1024 * 1024 * 128),
+            sample_desc="1 head x 1024 queries x 1024 keys", workload=dict(heads=32, seq=4096, dim=128)),
+        "c5-decoder": dict(
+            make=lambda: (W.decoder_program(), W.decoder_inputs()),
+            dtype="bf16", unit="TFLOP/s", bound="mfma", work=893353197568.0, peak=MFMA_PEAK_TFLOPS["bf16"],
+            sample=lambda: (W.decoder_program(1, 128), W.decoder_inputs(1, 128),
+                            2.0 * 128 * 2048 * (3 * 2048 + 2048 + 2 * 8192) + 2.0 * 16 * 128 * 128 * 128),
+            sample_desc="batch 1 x seq 128", workload=dict(batch=4, seq=2048, model=2048, heads=16, hd=128, ffn=8192)),
+    }
+
+
+def oracle_time(cfg, budget_s: float = 10.0):
+    """Times the CPU oracle on the config's bounded sample; repeats until `budget_s` is spent."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from conftest import oracle_lib, oracle_run
+    prog, ins, work = cfg["sample"]()
+    lib = oracle_lib()
+    threads = int(os.environ.get("ACCY_CPU_THREADS", "0")) or (os.cpu_count() or 1)
+    threads = min(threads, 16)
+    lib.accy_cpu_set_threads(threads)
+    times = []
+    start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle_run(prog, ins)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - start >= budget_s or len(times) >= 20:
+            break
+    t = float(np.median(times))
+    scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
+    return dict(value=work / t / scale, unit=cfg["unit"], cores=threads, kind="port",
+                sample=f"{cfg['sample_desc']}; median of {len(times)} runs, {t:.3f} s each")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c2-lse")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); the target runs on a single MI355X "
+              "and has no multi-GPU path.", file=sys.stderr)
+        return 2
+    import torch
+
+    cfgs = config_table()
+    cfg = cfgs[args.config]
+    prog, ins = cfg["make"]()
+    dev = torch.device("cuda:0")
+    dins = [torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in ins]
+    douts = [torch.zeros(t.byte_count(), dtype=torch.uint8, device=dev) for t in prog.output_types()]
+    del ins
+    stream = torch.cuda.current_stream()
+    ex = hip.Hip(prog)
+    iptr = [t.data_ptr() for t in dins]
+    optr = [t.data_ptr() for t in douts]
+
+    def step():
+        ex.launch_device(iptr, optr, stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+
+    # Per-kernel durations: HIP events recorded on the launch stream around each kernel.
+    ex.set_profiling(True)
+    per_kernel = {}
+    reps = max(3, min(args.steps, 10))
+    for _ in range(reps):
+        step()
+        for k in ex.kernels():
+            per_kernel.setdefault(k.label, []).append((k.last_ms, k))
+    ex.set_profiling(False)
+    dominant = max(per_kernel.items(), key=lambda kv: sum(m for m, _ in kv[1]))
+    dom_ms = float(np.mean([m for m, _ in dominant[1]]))
+    scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
+    value = cfg["work"] / (ms_per_step * 1e-3) / scale
+    if cfg["bound"] == "hbm":
+        achieved = cfg["work"] / (dom_ms * 1e-3) / 1e9
+        roof = dict(bound="hbm", achieved=achieved, peak=cfg["peak"], unit="GB/s", frac=achieved / cfg["peak"],
+                    traffic=None, kernel=dominant[0], kernel_ms=dom_ms)
+    else:
+        achieved = cfg["work"] / (dom_ms * 1e-3) / 1e12
+        peak = cfg["peak"] / 1000.0 if cfg["unit"] == "GFLOP/s" else cfg["peak"]
+        roof = dict(bound=cfg["bound"], achieved=achieved, peak=peak, unit="TFLOP/s", frac=achieved / peak,
+                    traffic=None, kernel=dominant[0], kernel_ms=dom_ms)
+    cpu = None if args.no_cpu else oracle_time(cfg)
+    line = {
+        "metric": METRIC, "value": value, "unit": cfg["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": cfg["dtype"], "data": "synthetic (seeded SplitMix64)",
+        "config": dict(workload=args.config, **cfg["workload"]),
+        "roofline": roof, "cpu_baseline": cpu,
+        "kernels": {lbl: float(np.mean([m for m, _ in v])) for lbl, v in per_kernel.items()},
+    }
+    ex.deinit()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

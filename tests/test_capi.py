@@ -1,0 +1,101 @@
+"""The C ABI on a host without a GPU: the library loads, exports every declared entry point, lowers
+every config program into kernels that hiprtc compiles for gfx950, and maps failures to the
+reference session's status numbers (src/tensor/session/session.zig:33-56)."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from accy_amd import hip
+from accy_amd import tensor as T
+from accy_amd import workloads as W
+from test_wire import readme_one_guess_bytes, u32
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "accy_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(accy_hip_\w+)\(", text, re.M)))
+
+
+def test_library_exports_every_declared_entry_point():
+    lib = hip.library()
+    names = declared_functions()
+    assert len(names) >= 13
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(hip.EXPORTS)
+
+
+SMALL_PROGRAMS = {
+    "readme": lambda: W.tone_program(points=16, scalar=True),
+    "tone": lambda: W.tone_program(64, 1024),
+    "lse": lambda: W.logsumexp_program(16, 8192),
+    "lse-bf16": lambda: W.logsumexp_program(16, 256, dtype="bf16"),
+    "gemm-f32": lambda: W.gemm_program(64, 64, 64),
+    "gemm-bf16-mulsum": lambda: W.gemm_program(64, 64, 64, "bf16", "mulsum"),
+    "attention": lambda: W.attention_program(2, 128, 64),
+    "attention-causal": lambda: W.attention_program(2, 128, 64, causal=True),
+    "decoder": lambda: W.decoder_program(1, 64, 128, 2, 64, 256),
+}
+
+
+@pytest.mark.parametrize("name", sorted(SMALL_PROGRAMS))
+def test_every_config_program_lowers_and_compiles_for_gfx950(name):
+    src = hip.plan_source(SMALL_PROGRAMS[name](), compile=True)
+    assert "__global__" in src
+
+
+def test_indexing_and_integer_programs_compile():
+    def body(b, a):
+        g = a[0].gather(a[1], "v")
+        return [a[0].scatter_add(a[1], g, "v"), a[2].add(a[2]).max("j")]
+    p = T.define("ix", [T.spec("f32", v=8), T.spec("i32", j=8), T.spec("i32", j=8)], body)
+    assert "__global__" in hip.plan_source(p, compile=True)
+
+
+def test_row_fusion_gives_one_kernel_for_logsumexp():
+    src = hip.plan_source(W.logsumexp_program(32, 8192))
+    assert src.count("__global__") == 1
+    assert "cache0" in src   # the row stays in registers between the max pass and the sum pass
+
+
+def _status_of_plan(wire: bytes) -> int:
+    lib = hip.library()
+    buf = (ctypes.c_uint8 * len(wire)).from_buffer_copy(wire)
+    need = ctypes.c_size_t()
+    return lib.accy_hip_plan_source(buf, len(wire), 0, None, 0, ctypes.byref(need))
+
+
+def test_bad_wire_bytes_map_to_session_statuses():
+    good = readme_one_guess_bytes()
+    assert _status_of_plan(good) == hip.OK
+    assert _status_of_plan(b"XCTP" + good[4:]) == hip.INVALID_PROGRAM
+    assert _status_of_plan(good[:4] + u32(7) + good[8:]) == hip.UNSUPPORTED_VERSION
+    assert _status_of_plan(good[:-2]) == hip.INVALID_PROGRAM
+
+
+def test_unknown_handles_are_refused():
+    lib = hip.library()
+    for h in (hip.Handle(0, 12345), hip.Handle(64, 0), hip.Handle(1000, 0)):
+        assert lib.accy_hip_release(h) == hip.INVALID_HANDLE
+        assert lib.accy_hip_counts(h, None, None) == hip.INVALID_HANDLE
+
+
+def test_unsupported_operations_fail_to_compile_with_a_named_reason():
+    p = T.define("ce", [T.spec("f32", r=2, c=3), T.spec("i32", r=2)],
+                 lambda b, a: a[0].sparse_cross_entropy_loss(a[1], "c"))
+    with pytest.raises(hip.HipError) as e:
+        hip.plan_source(p)
+    assert e.value.status == hip.COMPILE_FAILED and "sparse_cross_entropy" in e.value.message
+
+
+def test_compile_without_a_device_fails_loudly():
+    if hip.library().accy_hip_device_arch(None, 0) == hip.OK:
+        pytest.skip("a HIP device is present")
+    with pytest.raises(hip.HipError) as e:
+        hip.Hip(W.tone_program(8, 16))
+    assert e.value.status == hip.COMPILE_FAILED

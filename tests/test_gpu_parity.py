@@ -1,0 +1,249 @@
+"""Parity of the gfx950 target with the CPU oracle, through the C ABI, on an MI355X.
+
+Tolerances (BASELINE parity table): f32 reductions relative 1e-5 per element; f32 GEMM / attention
+1e-3 normwise plus per element with a floor; bf16 / f16 2e-2 in the same two forms; integer, index
+and i1 results, and 16-bit add/sub/mul/div chains, bit-exact.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from accy_amd import hip
+from accy_amd import tensor as T
+from accy_amd import workloads as W
+from conftest import assert_normwise, assert_rel, hip_run, oracle_run, out_arrays
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+# ---- README known answers (README.md:152-160; main.zig:200-228) ----
+
+def test_readme_tone_known_answers_on_gpu():
+    time, sample = W.readme_tone()
+    one = W.tone_program(points=16, scalar=True)
+    v25 = hip_run(one, [np.array(2.5, np.float32), time, sample])[0]
+    v3 = hip_run(one, [np.array(3.0, np.float32), time, sample])[0]
+    assert abs(float(v25) - 8.656) < 5e-4
+    assert abs(float(v3)) <= 1e-9
+    starts = np.array([0.5, 1.5, 2.5, 3.5, 4.5, 5.5, 6.5, 7.5], np.float32)
+    eight = hip_run(W.tone_program(8, 16), [starts, time, sample])[0]
+    ref = oracle_run(W.tone_program(8, 16), [starts, time, sample])[0]
+    assert_rel(eight, ref, 1e-5)
+
+
+# ---- C1 tone and C2 logsumexp ----
+
+def test_tone_subset_matches_oracle():
+    say("tone 512 x 16384")
+    prog = W.tone_program(512, 16384)
+    ins = W.tone_inputs(512, 16384, seed=1)
+    assert_rel(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-5)
+
+
+def test_logsumexp_subset_matches_oracle():
+    say("lse 1024 x 8192")
+    prog = W.logsumexp_program(1024, 8192)
+    ins = W.logsumexp_inputs(1024, 8192, seed=2)
+    assert_rel(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-5)
+
+
+@pytest.mark.parametrize("rows,features", [(3, 100), (5, 8), (7, 12289), (1, 1), (2, 64)])
+def test_logsumexp_ragged_shapes(rows, features):
+    say(f"lse {rows} x {features}")
+    prog = W.logsumexp_program(rows, features)
+    ins = W.logsumexp_inputs(rows, features, seed=rows + features)
+    assert_rel(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-5)
+
+
+def test_full_size_configs_on_sampled_rows():
+    """C1 and C2 at BASELINE sizes: every row is independent, so the oracle run on a sample of rows
+    (the same program over fewer rows) must match those rows of the full GPU result; all rows must
+    satisfy max <= lse <= max + log(features) and mismatch >= 0."""
+    rng = np.random.default_rng(0)
+    say("lse 32768 x 8192 (full)")
+    x = W.logsumexp_inputs(32768, 8192, seed=2)[0]
+    got = hip_run(W.logsumexp_program(32768, 8192), [x])[0]
+    m = x.max(axis=1)
+    assert (got >= m).all() and (got <= m + np.float32(math.log(8192) + 1e-3)).all()
+    rows = np.sort(rng.choice(32768, 256, replace=False))
+    ref = oracle_run(W.logsumexp_program(256, 8192), [x[rows]])[0]
+    assert_rel(got[rows], ref, 1e-5)
+    del x
+    say("tone 8192 x 16384 (full)")
+    f, t, s = W.tone_inputs(8192, 16384, seed=1)
+    got = hip_run(W.tone_program(8192, 16384), [f, t, s])[0]
+    assert (got >= 0).all()
+    idx = np.sort(rng.choice(8192, 128, replace=False))
+    ref = oracle_run(W.tone_program(128, 16384), [f[idx], t, s])[0]
+    assert_rel(got[idx], ref, 1e-5)
+
+
+# ---- row pipelines beyond logsumexp ----
+
+def test_softmax_full_row_output():
+    def body(b, a):
+        x = a[0]
+        e = x.sub(x.max("c")).exp()
+        return e.div(e.sum("c"))
+    prog = T.define("softmax", [T.spec("f32", r=64, c=1000)], body)
+    x = W.logsumexp_inputs(64, 1000, seed=9)[0]
+    assert_rel(hip_run(prog, [x])[0], oracle_run(prog, [x])[0], 1e-5)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_rms_norm(dtype):
+    prog = T.define("rms", [T.spec(dtype, b=2, s=33, model=2048), T.spec(dtype, model=2048)],
+                    lambda b, a: W.rms_norm(b, a[0], a[1], "model", dtype))
+    x = W.to_dtype(W.normal(4, 2 * 33 * 2048), dtype).reshape(2, 33, 2048)
+    g = W.to_dtype(W.uniform(5, 2048, 0.5, 1.5), dtype)
+    got, ref = hip_run(prog, [x, g])[0], oracle_run(prog, [x, g])[0]
+    assert_rel(got, ref, 1e-5 if dtype == "f32" else 2e-2, dtype)
+
+
+def test_reduction_over_leading_axis_uses_serial_fold_bit_exact():
+    prog = T.define("col", [T.spec("f32", k=300, n=77)], lambda b, a: a[0].sum("k"))
+    x = W.logsumexp_inputs(300, 77, seed=3)[0]
+    assert np.array_equal(hip_run(prog, [x])[0], oracle_run(prog, [x])[0])
+
+
+def test_multi_output_program_with_copies():
+    def body(b, a):
+        s = a[0].sum("c")
+        return [s, a[0], s, a[1].exp()]
+    prog = T.define("multi", [T.spec("f32", r=4, c=128), T.spec("f32", r=4)], body)
+    x = W.logsumexp_inputs(4, 128, seed=7)[0]
+    y = np.linspace(-1, 1, 4).astype(np.float32)
+    got, ref = hip_run(prog, [x, y]), oracle_run(prog, [x, y])
+    assert_rel(got[0], ref[0], 1e-5)
+    assert np.array_equal(got[1], x) and np.array_equal(got[2], got[0])
+    assert_rel(got[3], ref[3], 1e-6)
+
+
+# ---- contractions on the serial-k path: bit-exact with the oracle ----
+
+@pytest.mark.parametrize("dtype,spelling", [("f32", "contract"), ("f32", "mulsum"), ("bf16", "contract"),
+                                            ("f16", "mulsum")])
+def test_small_contractions(dtype, spelling):
+    prog = W.gemm_program(33, 65, 17, dtype, spelling)
+    ins = W.gemm_inputs(33, 65, 17, dtype, seed=5)
+    got, ref = hip_run(prog, ins)[0], oracle_run(prog, ins)[0]
+    assert_normwise(got, ref, 1e-3 if dtype == "f32" else 2e-2, dtype)
+
+
+def test_small_attention_and_decoder():
+    prog = W.attention_program(2, 64, 32, "f16", causal=True)
+    ins = W.attention_inputs(2, 64, 32, "f16", seed=6)
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "f16")
+    prog = W.decoder_program(1, 16, 64, 2, 32, 128, dtype="bf16")
+    ins = W.decoder_inputs(1, 16, 64, 2, 32, 128, dtype="bf16", seed=7)
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16")
+
+
+# ---- exact classes ----
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_16bit_arithmetic_chains_bit_exact(dtype):
+    def body(b, a):
+        return a[0].mul(a[1]).add(a[0]).sub(a[1].div(a[0]))
+    prog = T.define("ch", [T.spec(dtype, i=4096), T.spec(dtype, i=4096)], body)
+    ins = [W.to_dtype(W.normal(11, 4096) * 3, dtype), W.to_dtype(W.normal(12, 4096), dtype)]
+    got, ref = hip_run(prog, ins)[0], oracle_run(prog, ins)[0]
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def test_integer_compare_select_gather_scatter_exact():
+    def body(b, a):
+        x, idx, v = a
+        g = x.gather(idx, "v")
+        sc = x.scatter_add(idx, v, "v")
+        mask = v.compare("gt", b.full("i32", 0, j=9))
+        return [g, sc, mask.select(v.add(v), v.neg()), v.max("j"), v.div(b.full("i32", 3, j=9))]
+    prog = T.define("ints", [T.spec("i32", v=6), T.spec("i32", j=9), T.spec("i32", j=9)], body)
+    x = np.array([5, -3, 2 ** 31 - 1, 0, 7, -9], np.int32)
+    idx = np.array([0, 5, 9, -2, 3, 3, 1, 2, 2], np.int32)
+    v = np.array([1, -2, 3, 2 ** 30, -5, 6, 7, -8, 9], np.int32)
+    got, ref = hip_run(prog, [x, idx, v]), oracle_run(prog, [x, idx, v])
+    for g, r in zip(got, ref):
+        assert np.array_equal(g, r)
+
+
+def test_zero_sized_and_scalar_programs():
+    prog = T.define("z", [T.spec("f32", a=0, b=4), T.spec("f32")], lambda b, a: [a[0].sum("a"), a[1].exp()])
+    got = hip_run(prog, [np.zeros((0, 4), np.float32), np.array(1.0, np.float32)])
+    assert np.array_equal(got[0], np.zeros(4, np.float32))
+    assert abs(float(got[1]) - math.e) < 1e-6
+
+
+# ---- session semantics (session.zig:99-246) ----
+
+def test_session_descriptors_invoke_release():
+    s = hip.Session()
+    prog = W.logsumexp_program(8, 256)
+    h = s.compile(prog)
+    ins, outs = s.input_descriptors(h), s.output_descriptors(h)
+    assert ins[0].dtype == "f32" and ins[0].dims == (("row", 8), ("feature", 256))
+    assert ins[0].byte_size == 8 * 256 * 4 and outs[0].dims == (("row", 8),)
+    x = W.logsumexp_inputs(8, 256)[0]
+    out = np.zeros(8, np.float32)
+    s.invoke(h, [x], [out])
+    assert_rel(out, oracle_run(prog, [x])[0], 1e-5)
+    with pytest.raises(hip.HipError) as e:
+        s.invoke(h, [x[:4]], [out])
+    assert e.value.status == hip.INVALID_BUFFER
+    with pytest.raises(hip.HipError) as e:
+        s.invoke(h, [x], [np.zeros(9, np.float32)])
+    assert e.value.status == hip.INVALID_BUFFER
+    with pytest.raises(hip.HipError) as e:
+        s.invoke(h, [x, x], [out])
+    assert e.value.status == hip.INVALID_BUFFER
+    alias = np.zeros(8 * 256, np.float32)
+    with pytest.raises(hip.HipError) as e:
+        s.invoke(h, [alias], [alias[:8]])
+    assert e.value.status == hip.INVALID_BUFFER
+    s.release(h)
+    with pytest.raises(hip.HipError) as e:
+        s.invoke(h, [x], [out])
+    assert e.value.status == hip.INVALID_HANDLE
+    h2 = s.compile(prog)
+    assert h2.index == h.index and h2.generation == h.generation + 1
+    s.release(h2)
+
+
+def test_table_holds_at_most_64_programs():
+    s = hip.Session()
+    prog = W.tone_program(8, 16)
+    hs = [s.compile(prog) for _ in range(64)]
+    with pytest.raises(hip.HipError) as e:
+        s.compile(prog)
+    assert e.value.status == hip.TOO_MANY_PROGRAMS
+    for h in hs:
+        s.release(h)
+
+
+def test_executor_launches_many_times_and_device_invoke():
+    torch = pytest.importorskip("torch")
+    prog = W.logsumexp_program(64, 4096)
+    x = W.logsumexp_inputs(64, 4096, seed=13)[0]
+    ref = oracle_run(prog, [x])[0]
+    with hip.Hip(prog) as ex:
+        for _ in range(3):
+            out = np.zeros(64, np.float32)
+            ex.launch([x], [out])
+            assert_rel(out, ref, 1e-5)
+        dx = torch.from_numpy(x).to("cuda:0")
+        dout = torch.zeros(64, dtype=torch.float32, device="cuda:0")
+        stream = torch.cuda.current_stream()
+        ex.launch_device([dx.data_ptr()], [dout.data_ptr()], stream.cuda_stream)
+        stream.synchronize()
+        assert_rel(dout.cpu().numpy(), ref, 1e-5)
+
+
+def test_bad_wire_is_refused_by_compile():
+    with pytest.raises(hip.HipError) as e:
+        hip.Session().compile(b"ACTP\x02\x00\x00\x00")
+    assert e.value.status == hip.UNSUPPORTED_VERSION

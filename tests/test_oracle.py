@@ -1,0 +1,326 @@
+"""Pins the CPU oracle (the runCpu restatement) before anything is compared against it.
+
+Each check is chosen so that a plausible mistake in the restatement fails it: a pairwise or f64
+accumulation instead of the serial f32 fold, a fused multiply-add, a dropped term, a transposed
+operand, a wrong rounding of 16-bit results, unclamped gather indices.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from accy_amd import tensor as T
+from accy_amd import workloads as W
+from conftest import oracle_lib, oracle_run
+
+
+def f64_mismatch(time, sample, frequency):
+    """examples/consumer/src/main.zig:187-198: the mismatch and its slope in f64."""
+    t = time.astype(np.float64)
+    d = np.sin(frequency * t) - sample.astype(np.float64)
+    return (d * d).sum(), (2 * d * np.cos(frequency * t) * t).sum()
+
+
+# ---- known answers of the reference (README.md:152-160, 300-304; main.zig:200-228) ----
+
+def test_readme_tone_known_answers():
+    time, sample = W.readme_tone()
+    one = W.tone_program(points=16, scalar=True)
+    v25 = oracle_run(one, [np.array(2.5, np.float32), time, sample])[0]
+    v3 = oracle_run(one, [np.array(3.0, np.float32), time, sample])[0]
+    assert abs(float(v25) - 8.656) < 5e-4                       # README.md:152, 160 "about 8.656"
+    ref, slope = f64_mismatch(time, sample, 2.5)
+    assert abs(float(v25) - ref) <= 1e-5 * abs(ref)             # main.zig:208
+    assert abs(float(v3)) <= 1e-9                               # main.zig:210
+    assert abs(slope - (-31.29)) < 5e-3                         # README.md:300
+
+
+def test_eight_guesses_equal_eight_single_runs():
+    time, sample = W.readme_tone()
+    starts = np.array([0.5, 1.5, 2.5, 3.5, 4.5, 5.5, 6.5, 7.5], np.float32)
+    eight = oracle_run(W.tone_program(guesses=8, points=16), [starts, time, sample])[0]
+    one = W.tone_program(points=16, scalar=True)
+    for s, v in zip(starts, eight):
+        alone = oracle_run(one, [np.array(s, np.float32), time, sample])[0]
+        assert abs(float(alone) - float(v)) <= 1e-6 * abs(float(alone))   # main.zig:213-228
+        assert abs(float(v) - f64_mismatch(time, sample, float(s))[0]) <= 1e-5 * abs(float(v))
+
+
+def test_mismatch_curve_361_points_against_f64():
+    """The README's figure data: 361 guesses from -0.5 to 8.5 (main.zig:152-181)."""
+    time, sample = W.readme_tone()
+    freq = (-0.5 + 0.025 * np.arange(361)).astype(np.float32)
+    got = oracle_run(W.tone_program(guesses=361, points=16), [freq, time, sample])[0]
+    for f, v in zip(freq, got):
+        ref = f64_mismatch(time, sample, float(f))[0]
+        assert abs(float(v) - ref) <= 1e-5 * abs(ref) + 1e-9
+
+
+# ---- fold order (reduction.zig:839-878, 1157-1177) ----
+
+def _sum_program(n, dtype="f32"):
+    return T.define("s", [T.spec(dtype, i=n)], lambda b, a: a[0].sum("i"))
+
+
+def test_sum_is_a_serial_left_to_right_f32_fold():
+    # Serial f32: ((1e8 + 1) - 1e8) + 1 = 1; pairwise gives 0; f64 accumulation gives 2.
+    x = np.array([1e8, 1.0, -1e8, 1.0], np.float32)
+    assert float(oracle_run(_sum_program(4), [x])[0]) == 1.0
+
+
+def test_sum_matches_explicit_serial_loop_bit_exact():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((5, 333)).astype(np.float32)
+    prog = T.define("s", [T.spec("f32", a=5, b=333)], lambda b, a: a[0].sum("b"))
+    got = oracle_run(prog, [x])[0]
+    for r in range(5):
+        acc = np.float32(0)
+        for v in x[r]:
+            acc = np.float32(acc + v)
+        assert got[r] == acc
+
+
+def test_multi_axis_reduce_folds_in_row_major_order_of_reduced_axes():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((3, 4, 5)) * 1e4).astype(np.float32)
+    prog = T.define("s", [T.spec("f32", a=3, b=4, c=5)], lambda b, a: a[0].sum(("a", "c")))
+    got = oracle_run(prog, [x])[0]
+    for j in range(4):
+        acc = np.float32(0)
+        for i in range(3):
+            for k in range(5):
+                acc = np.float32(acc + x[i, j, k])
+        assert got[j] == acc
+
+
+def test_max_and_min_reduce():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((7, 64)).astype(np.float32)
+    mx = T.define("m", [T.spec("f32", r=7, c=64)], lambda b, a: [a[0].max("c"), a[0].min("r")])
+    got = oracle_run(mx, [x])
+    assert np.array_equal(got[0], x.max(axis=1))
+    assert np.array_equal(got[1], x.min(axis=0))
+
+
+def test_f16_sum_widens_to_f32_and_rounds_once():
+    # 4096 ones in f16: an f16 accumulator sticks at 2048; the f32 accumulator reaches 4096.
+    x = np.ones(4096, np.float16)
+    assert float(oracle_run(_sum_program(4096, "f16"), [x])[0]) == 4096.0
+
+
+# ---- elementwise arithmetic and 16-bit rounding (src/eval/root.zig:10-16) ----
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div"])
+def test_f16_binary_ops_round_to_nearest_even_after_each_op(op):
+    rng = np.random.default_rng(3)
+    a = (rng.standard_normal(4096) * np.exp(rng.uniform(-12, 12, 4096))).astype(np.float16)
+    b = (rng.standard_normal(4096) * np.exp(rng.uniform(-12, 12, 4096))).astype(np.float16)
+    prog = T.define("e", [T.spec("f16", i=4096), T.spec("f16", i=4096)], lambda bb, x: getattr(x[0], op)(x[1]))
+    got = oracle_run(prog, [a, b])[0]
+    # numpy computes float16 arithmetic in f32 and rounds the result to nearest even.
+    ref = getattr(np, {"add": "add", "sub": "subtract", "mul": "multiply", "div": "divide"}[op])(a, b)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)) or np.array_equal(
+        np.nan_to_num(got.astype(np.float32)), np.nan_to_num(ref.astype(np.float32)))
+
+
+def test_bf16_ops_round_to_nearest_even():
+    rng = np.random.default_rng(4)
+    a32 = rng.standard_normal(2048).astype(np.float32)
+    b32 = rng.standard_normal(2048).astype(np.float32)
+    a, b = W.to_dtype(a32, "bf16"), W.to_dtype(b32, "bf16")
+    prog = T.define("e", [T.spec("bf16", i=2048), T.spec("bf16", i=2048)], lambda bb, x: x[0].mul(x[1]))
+    got = oracle_run(prog, [a, b])[0]
+    exact = W.bf16_to_f32(a).astype(np.float64) * W.bf16_to_f32(b).astype(np.float64)
+    ref = W.to_dtype(exact.astype(np.float32), "bf16")   # product exact in f32, then RNE to bf16
+    assert np.array_equal(got, ref)
+
+
+def test_unary_f32_ops_against_f64():
+    rng = np.random.default_rng(5)
+    x = rng.uniform(0.1, 20.0, 1024).astype(np.float32)
+    for name, f in [("exp", np.exp), ("log", np.log), ("sqrt", np.sqrt), ("tanh", np.tanh), ("sin", np.sin),
+                    ("cos", np.cos), ("neg", np.negative), ("abs", np.abs)]:
+        prog = T.define("u", [T.spec("f32", i=1024)], lambda b, a, n=name: getattr(a[0], n)())
+        got = oracle_run(prog, [x])[0].astype(np.float64)
+        ref = f(x.astype(np.float64))
+        ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+        assert (np.abs(got - ref) <= 2 * ulp).all(), name
+
+
+def test_no_fused_multiply_add_in_elementwise_chains():
+    # a*b + c with a*b rounded first: chosen so that FMA gives a different f32 result.
+    a = np.array([1.0 + 2.0 ** -12], np.float32)
+    c = np.array([-(1.0 + 2.0 ** -11)], np.float32)
+    prog = T.define("f", [T.spec("f32", i=1)] * 3, lambda b, x: x[0].mul(x[1]).add(x[2]))
+    got = oracle_run(prog, [a, a, c])[0]
+    separate = np.float32(np.float32(a[0] * a[0]) + c[0])
+    fused = np.float32(np.float64(a[0]) * np.float64(a[0]) + np.float64(c[0]))
+    assert separate != fused
+    assert got[0] == separate
+
+
+def test_integer_arithmetic_wraps_and_divides_toward_zero():
+    x = np.array([2 ** 31 - 1, -7, 7, -(2 ** 31)], np.int32)
+    y = np.array([1, 2, -2, -1], np.int32)
+    prog = T.define("i", [T.spec("i32", i=4)] * 2, lambda b, a: [a[0].add(a[1]), a[0].div(a[1])])
+    s, q = oracle_run(prog, [x, y])
+    assert list(s) == [-(2 ** 31), -5, 5, 2 ** 31 - 1]
+    assert list(q) == [2 ** 31 - 1, -3, -3, -(2 ** 31)]
+
+
+# ---- contraction (dot.zig:2049-2115) ----
+
+def test_dot_general_matches_serial_k_loop_bit_exact():
+    rng = np.random.default_rng(6)
+    a = rng.uniform(-1, 1, (6, 37)).astype(np.float32)
+    b = rng.uniform(-1, 1, (37, 5)).astype(np.float32)
+    got = oracle_run(W.gemm_program(6, 37, 5), [a, b])[0]
+    for i in range(6):
+        for j in range(5):
+            acc = np.float32(0)
+            for k in range(37):
+                acc = np.float32(acc + np.float32(a[i, k] * b[k, j]))
+            assert got[i, j] == acc
+    assert np.abs(got - a.astype(np.float64) @ b.astype(np.float64)).max() < 1e-5
+
+
+def test_mul_sum_spelling_equals_contract_spelling():
+    rng = np.random.default_rng(7)
+    a, b = W.gemm_inputs(9, 33, 7, seed=11)
+    c1 = oracle_run(W.gemm_program(9, 33, 7, spelling="contract"), [a, b])[0]
+    c2 = oracle_run(W.gemm_program(9, 33, 7, spelling="mulsum"), [a, b])[0]
+    assert np.array_equal(c1, c2)
+
+
+def test_batched_transposed_contraction_against_einsum():
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal((3, 4, 8)).astype(np.float32)    # head, query, dim
+    k = rng.standard_normal((3, 5, 8)).astype(np.float32)    # head, key, dim
+    prog = T.define("qk", [T.spec("f32", head=3, query=4, dim=8), T.spec("f32", head=3, key=5, dim=8)],
+                    lambda b, a: a[0].contract(a[1], "dim"))
+    got = oracle_run(prog, [q, k])[0]
+    ref = np.einsum("hqd,hkd->hqk", q.astype(np.float64), k.astype(np.float64))
+    assert np.abs(got - ref).max() < 1e-5
+
+
+def test_f16_contraction_accumulates_in_f32():
+    # 4096 products of 1*1 in f16: an f16 accumulator would stop at 2048.
+    a = np.ones((1, 4096), np.float16)
+    b = np.ones((4096, 1), np.float16)
+    assert float(oracle_run(W.gemm_program(1, 4096, 1, dtype="f16"), [a, b])[0][0, 0]) == 4096.0
+
+
+# ---- attention, LSE, GELU closed forms ----
+
+def test_attention_matches_reference_sdpa_closed_form():
+    """src/kernel/library/attention.zig:464-509 (2 batches, 2 queries, 3 keys, qk 2, value 2)."""
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((2, 2, 2)).astype(np.float32)
+    k = rng.standard_normal((2, 3, 2)).astype(np.float32)
+    v = rng.standard_normal((2, 3, 2)).astype(np.float32)
+
+    def body(b, a):
+        s = a[0].contract(a[1], "qk").mul(b.full_float(T.Type("f32", ()), 1.0 / math.sqrt(2)))
+        e = s.sub(s.max("key")).exp()
+        return e.div(e.sum("key")).contract(a[2], "key")
+    prog = T.define("sdpa", [T.spec("f32", batch=2, query=2, qk=2), T.spec("f32", batch=2, key=3, qk=2),
+                             T.spec("f32", batch=2, key=3, value=2)], body)
+    got = oracle_run(prog, [q, k, v])[0]
+    scale = np.float32(1.0 / math.sqrt(2.0))
+    for bi in range(2):
+        for qi in range(2):
+            sc = [np.float32(np.float32(q[bi, qi, 0] * k[bi, j, 0]) + np.float32(q[bi, qi, 1] * k[bi, j, 1])) * scale
+                  for j in range(3)]
+            m = max(sc)
+            den = np.float32(0)
+            for s_ in sc:
+                den = np.float32(den + np.exp(np.float32(s_ - m)))
+            for vi in range(2):
+                acc = np.float32(0)
+                for j in range(3):
+                    acc = np.float32(acc + np.float32(np.float32(np.exp(np.float32(sc[j] - m)) / den) * v[bi, j, vi]))
+                assert abs(got[bi, qi, vi] - acc) <= 1e-6 * max(1.0, abs(acc))
+
+
+def test_logsumexp_against_f64():
+    x = W.logsumexp_inputs(64, 1024, seed=21)[0]
+    got = oracle_run(W.logsumexp_program(64, 1024), [x])[0]
+    x64 = x.astype(np.float64)
+    m = x64.max(axis=1)
+    ref = m + np.log(np.exp(x64 - m[:, None]).sum(axis=1))
+    assert np.abs(got - ref).max() <= 1e-6 * np.abs(ref).max()
+
+
+def test_gelu_tanh_approximation_on_eight_values():
+    """src/kernel/library/fused.zig:471-478 / elementwise.zig:234-240."""
+    x = np.array([-3.0, -1.5, -0.5, -0.1, 0.0, 0.3, 1.0, 2.5], np.float32)
+    prog = T.define("g", [T.spec("f32", i=8)], lambda b, a: W.gelu(b, a[0], "f32"))
+    got = oracle_run(prog, [x])[0]
+    x64 = x.astype(np.float64)
+    ref = 0.5 * x64 * (1 + np.tanh(0.7978845608028654 * (x64 + 0.044715 * x64 ** 3)))
+    assert np.abs(got - ref).max() <= 1e-6
+
+
+def test_rms_norm_against_f64():
+    rng = np.random.default_rng(10)
+    x = rng.standard_normal((4, 64)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, 64).astype(np.float32)
+    prog = T.define("n", [T.spec("f32", r=4, model=64), T.spec("f32", model=64)],
+                    lambda b, a: W.rms_norm(b, a[0], a[1], "model", "f32"))
+    got = oracle_run(prog, [x, g])[0]
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * g
+    assert np.abs(got - ref).max() <= 1e-5
+
+
+# ---- indexing ----
+
+def test_gather_clamps_indices_into_range():
+    x = np.arange(10, dtype=np.float32) * 10
+    idx = np.array([-5, 0, 3, 9, 12], np.int32)
+    prog = T.define("g", [T.spec("f32", v=10), T.spec("i32", j=5)], lambda b, a: a[0].gather(a[1], "v"))
+    assert list(oracle_run(prog, [x, idx])[0]) == [0, 0, 30, 90, 90]
+
+
+def test_scatter_add_accumulates_in_update_order():
+    x = np.zeros(4, np.float32)
+    idx = np.array([1, 1, 3, 1], np.int32)
+    upd = np.array([1e8, 1.0, 5.0, -1e8], np.float32)
+    prog = T.define("s", [T.spec("f32", v=4), T.spec("i32", j=4), T.spec("f32", j=4)],
+                    lambda b, a: a[0].scatter_add(a[1], a[2], "v"))
+    got = oracle_run(prog, [x, idx, upd])[0]
+    assert list(got) == [0.0, 0.0, 0.0, 5.0]   # ((1e8 + 1) - 1e8) = 0 in serial f32
+
+
+def test_decoder_block_small_against_f64():
+    """A scaled-down decoder block in f32: every op of the traced program is checked against an
+    independent f64 formulation (no dropped residual, mask, or norm)."""
+    B, S, M, H, D, F = 2, 8, 16, 2, 8, 32
+    ins = W.decoder_inputs(B, S, M, H, D, F, dtype="f32", seed=31)
+    got = oracle_run(W.decoder_program(B, S, M, H, D, F, dtype="f32"), ins)[0].astype(np.float64)
+    x, g1, wq, wk, wv, wo, g2, w1, w2 = [a.astype(np.float64) for a in ins]
+
+    def rms(t, g):
+        return t / np.sqrt((t * t).mean(-1, keepdims=True) + 1e-5) * g
+    h = rms(x, g1)
+    q = np.einsum("bsm,mhd->bshd", h, wq)
+    k = np.einsum("bsm,mhd->bshd", h, wk)
+    v = np.einsum("bsm,mhd->bshd", h, wv)
+    s = np.einsum("bqhd,bkhd->bhqk", q, k) / math.sqrt(D)
+    s = np.where(np.tril(np.ones((S, S), bool)), s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    o = np.einsum("bhqk,bkhd->bhqd", p, v)
+    x1 = x + np.einsum("bhsd,hdm->bsm", o, wo)
+    f = np.einsum("bsm,mf->bsf", rms(x1, g2), w1)
+    f = 0.5 * f * (1 + np.tanh(0.7978845608028654 * (f + 0.044715 * f ** 3)))
+    ref = x1 + np.einsum("bsf,fm->bsm", f, w2)
+    assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+
+
+def test_oracle_threads_give_identical_results():
+    x = W.logsumexp_inputs(256, 512, seed=5)[0]
+    prog = W.logsumexp_program(256, 512)
+    one = oracle_run(prog, [x], threads=1)[0]
+    many = oracle_run(prog, [x], threads=8)[0]
+    assert np.array_equal(one, many)

@@ -323,6 +323,55 @@ int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile
   });
 }
 
+static int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ACCY_HIP_OK;
+  return fail_with(e == hipErrorOutOfMemory ? ACCY_HIP_OUT_OF_MEMORY : ACCY_HIP_LAUNCH_FAILED,
+                   std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int accy_hip_malloc(void** ptr, size_t bytes) {
+  if (!ptr) return fail_with(ACCY_HIP_INVALID_BUFFER, "null pointer");
+  *ptr = nullptr;
+  if (bytes == 0) return ACCY_HIP_OK;
+  return hip_status(hipMalloc(ptr, bytes), "hipMalloc");
+}
+
+int accy_hip_free(void* ptr) { return ptr ? hip_status(hipFree(ptr), "hipFree") : ACCY_HIP_OK; }
+
+int accy_hip_memcpy(void* dst, const void* src, size_t bytes, int kind) {
+  if (bytes == 0) return ACCY_HIP_OK;
+  hipMemcpyKind k = kind == 1 ? hipMemcpyHostToDevice : kind == 2 ? hipMemcpyDeviceToHost : hipMemcpyDeviceToDevice;
+  if (kind < 1 || kind > 3) return fail_with(ACCY_HIP_INVALID_BUFFER, "copy kind must be 1, 2 or 3");
+  return hip_status(hipMemcpy(dst, src, bytes, k), "hipMemcpy");
+}
+
+int accy_hip_stream_create(void** stream) {
+  if (!stream) return fail_with(ACCY_HIP_INVALID_BUFFER, "null pointer");
+  return hip_status(hipStreamCreate((hipStream_t*)stream), "hipStreamCreate");
+}
+
+int accy_hip_stream_destroy(void* stream) { return hip_status(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy"); }
+
+int accy_hip_stream_synchronize(void* stream) {
+  return hip_status(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+int accy_hip_event_create(void** event) {
+  if (!event) return fail_with(ACCY_HIP_INVALID_BUFFER, "null pointer");
+  return hip_status(hipEventCreate((hipEvent_t*)event), "hipEventCreate");
+}
+
+int accy_hip_event_destroy(void* event) { return hip_status(hipEventDestroy((hipEvent_t)event), "hipEventDestroy"); }
+
+int accy_hip_event_record(void* event, void* stream) {
+  return hip_status(hipEventRecord((hipEvent_t)event, (hipStream_t)stream), "hipEventRecord");
+}
+
+int accy_hip_event_elapsed_ms(float* ms, void* start, void* end) {
+  if (!ms) return fail_with(ACCY_HIP_INVALID_BUFFER, "null pointer");
+  return hip_status(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)end), "hipEventElapsedTime");
+}
+
 int accy_hip_device_arch(char* buf, size_t cap) {
   return guarded([&]() -> int {
     if (device_count() <= 0) return fail_with(ACCY_HIP_LAUNCH_FAILED, "no HIP device");

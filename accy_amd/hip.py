@@ -85,7 +85,10 @@ _lib_lock = threading.Lock()
 
 EXPORTS = ["accy_hip_run", "accy_hip_compile", "accy_hip_counts", "accy_hip_describe", "accy_hip_invoke",
            "accy_hip_invoke_device", "accy_hip_release", "accy_hip_last_error", "accy_hip_set_profiling",
-           "accy_hip_kernel_count", "accy_hip_kernel_info", "accy_hip_plan_source", "accy_hip_device_arch"]
+           "accy_hip_kernel_count", "accy_hip_kernel_info", "accy_hip_plan_source", "accy_hip_device_arch",
+           "accy_hip_malloc", "accy_hip_free", "accy_hip_memcpy", "accy_hip_stream_create",
+           "accy_hip_stream_destroy", "accy_hip_stream_synchronize", "accy_hip_event_create",
+           "accy_hip_event_destroy", "accy_hip_event_record", "accy_hip_event_elapsed_ms"]
 
 
 def library() -> ctypes.CDLL:
@@ -112,6 +115,16 @@ def library() -> ctypes.CDLL:
         lib.accy_hip_kernel_info.argtypes = [Handle, sz, ctypes.POINTER(_KernelStats)]
         lib.accy_hip_plan_source.argtypes = [u8p, sz, ctypes.c_int, ctypes.c_char_p, sz, szp]
         lib.accy_hip_device_arch.argtypes = [ctypes.c_char_p, sz]
+        lib.accy_hip_malloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), sz]
+        lib.accy_hip_free.argtypes = [vp]
+        lib.accy_hip_memcpy.argtypes = [vp, vp, sz, ctypes.c_int]
+        lib.accy_hip_stream_create.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        lib.accy_hip_stream_destroy.argtypes = [vp]
+        lib.accy_hip_stream_synchronize.argtypes = [vp]
+        lib.accy_hip_event_create.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        lib.accy_hip_event_destroy.argtypes = [vp]
+        lib.accy_hip_event_record.argtypes = [vp, vp]
+        lib.accy_hip_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
         for name in EXPORTS:
             if name != "accy_hip_last_error":
                 getattr(lib, name).restype = ctypes.c_int
@@ -294,6 +307,83 @@ def device_arch() -> str:
     buf = ctypes.create_string_buffer(256)
     _check(library().accy_hip_device_arch(buf, 256))
     return buf.value.decode()
+
+
+class DeviceBuffer:
+    """Device memory from the library's own HIP runtime (``accy_hip_malloc``)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _check(library().accy_hip_malloc(ctypes.byref(p), self.nbytes))
+        self.ptr = p.value or 0
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(a.nbytes)
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        if a.nbytes != self.nbytes:
+            raise HipError(INVALID_BUFFER, "size mismatch")
+        _check(library().accy_hip_memcpy(self.ptr, a.ctypes.data, self.nbytes, 1))
+
+    def download(self, out: np.ndarray) -> np.ndarray:
+        if out.nbytes != self.nbytes or not out.flags.c_contiguous:
+            raise HipError(INVALID_BUFFER, "size mismatch")
+        _check(library().accy_hip_memcpy(out.ctypes.data, self.ptr, self.nbytes, 2))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            library().accy_hip_free(self.ptr)
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Stream:
+    """A HIP stream at the default priority."""
+
+    def __init__(self):
+        p = ctypes.c_void_p()
+        _check(library().accy_hip_stream_create(ctypes.byref(p)))
+        self.handle = p.value or 0
+
+    def synchronize(self) -> None:
+        _check(library().accy_hip_stream_synchronize(self.handle))
+
+    def destroy(self) -> None:
+        if self.handle:
+            library().accy_hip_stream_destroy(self.handle)
+            self.handle = 0
+
+
+class Event:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        _check(library().accy_hip_event_create(ctypes.byref(p)))
+        self.handle = p.value or 0
+
+    def record(self, stream: "Stream") -> None:
+        _check(library().accy_hip_event_record(self.handle, stream.handle if stream else 0))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _check(library().accy_hip_event_elapsed_ms(ctypes.byref(ms), self.handle, end.handle))
+        return float(ms.value)
+
+    def destroy(self) -> None:
+        if self.handle:
+            library().accy_hip_event_destroy(self.handle)
+            self.handle = 0
 
 
 def empty_output(desc: Descriptor) -> np.ndarray:

@@ -3,7 +3,7 @@
 ``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2-lse]`` prints ONE JSON line.
 
 * A step is one launch of the compiled program (``Hip.launch_device``) over inputs already resident
-  in HBM, on torch's current stream; K steps are timed between two synchronisations.
+  in HBM, on one HIP stream; K steps are timed between two synchronisations.
 * ``value`` is the whole-job throughput of the step: algorithmic bytes (HBM-bound configs) or
   algorithmic FLOP (MFMA / VALU-bound configs) per second, with the per-config figures of the
   measurement plan.
@@ -118,32 +118,33 @@ def main() -> int:
         print(f"bench.py measures one GPU only (asked for {args.gpus}); the target runs on a single MI355X "
               "and has no multi-GPU path.", file=sys.stderr)
         return 2
-    import torch
-
     cfgs = config_table()
     cfg = cfgs[args.config]
     prog, ins = cfg["make"]()
-    dev = torch.device("cuda:0")
-    dins = [torch.from_numpy(np.ascontiguousarray(x)).to(dev) for x in ins]
-    douts = [torch.zeros(t.byte_count(), dtype=torch.uint8, device=dev) for t in prog.output_types()]
+    # Inputs are copied into HBM before the timed region; outputs stay on the device.
+    dins = [hip.DeviceBuffer.from_array(x) for x in ins]
+    douts = [hip.DeviceBuffer(t.byte_count()) for t in prog.output_types()]
     del ins
-    stream = torch.cuda.current_stream()
+    stream = hip.Stream()
     ex = hip.Hip(prog)
-    iptr = [t.data_ptr() for t in dins]
-    optr = [t.data_ptr() for t in douts]
+    iptr = [b.ptr for b in dins]
+    optr = [b.ptr for b in douts]
 
     def step():
-        ex.launch_device(iptr, optr, stream.cuda_stream)
+        ex.launch_device(iptr, optr, stream.handle)
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
+    stream.synchronize()
+    start, end = hip.Event(), hip.Event()
     t0 = time.perf_counter()
+    start.record(stream)
     for _ in range(args.steps):
         step()
-    torch.cuda.synchronize()
+    end.record(stream)
+    stream.synchronize()
     elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
+    ms_per_step = max(elapsed * 1e3, start.elapsed_ms(end)) / args.steps
 
     # Per-kernel durations: HIP events recorded on the launch stream around each kernel.
     ex.set_profiling(True)
@@ -177,6 +178,8 @@ def main() -> int:
         "kernels": {lbl: float(np.mean([m for m, _ in v])) for lbl, v in per_kernel.items()},
     }
     ex.deinit()
+    for b in dins + douts:
+        b.free()
     print(json.dumps(line), flush=True)
     return 0
 

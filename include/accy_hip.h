@@ -113,6 +113,22 @@ int accy_hip_plan_source(const uint8_t* wire, size_t wire_len, int compile, char
 /* Name of the current HIP device's architecture (e.g. "gfx950:sramecc+:xnack-"). */
 int accy_hip_device_arch(char* buf, size_t cap);
 
+/* Device memory, streams and events of the runtime this library is linked against, for callers
+ * that keep inputs and outputs resident in HBM (the buffer half of the backend vtable:
+ * allocate_buffer / write_buffer / read_buffer / synchronize / destroy_object,
+ * deps/lib/compiler/gpu/src/contract.zig:2048-2084). `kind`: 1 host to device, 2 device to host,
+ * 3 device to device. All streams are created at the default priority. */
+int accy_hip_malloc(void** ptr, size_t bytes);
+int accy_hip_free(void* ptr);
+int accy_hip_memcpy(void* dst, const void* src, size_t bytes, int kind);
+int accy_hip_stream_create(void** stream);
+int accy_hip_stream_destroy(void* stream);
+int accy_hip_stream_synchronize(void* stream);
+int accy_hip_event_create(void** event);
+int accy_hip_event_destroy(void* event);
+int accy_hip_event_record(void* event, void* stream);
+int accy_hip_event_elapsed_ms(float* ms, void* start, void* end);
+
 #ifdef __cplusplus
 }
 #endif

@@ -226,7 +226,6 @@ def test_table_holds_at_most_64_programs():
 
 
 def test_executor_launches_many_times_and_device_invoke():
-    torch = pytest.importorskip("torch")
     prog = W.logsumexp_program(64, 4096)
     x = W.logsumexp_inputs(64, 4096, seed=13)[0]
     ref = oracle_run(prog, [x])[0]
@@ -235,12 +234,23 @@ def test_executor_launches_many_times_and_device_invoke():
             out = np.zeros(64, np.float32)
             ex.launch([x], [out])
             assert_rel(out, ref, 1e-5)
-        dx = torch.from_numpy(x).to("cuda:0")
-        dout = torch.zeros(64, dtype=torch.float32, device="cuda:0")
-        stream = torch.cuda.current_stream()
-        ex.launch_device([dx.data_ptr()], [dout.data_ptr()], stream.cuda_stream)
+        dx = hip.DeviceBuffer.from_array(x)
+        dout = hip.DeviceBuffer(64 * 4)
+        stream = hip.Stream()
+        start, end = hip.Event(), hip.Event()
+        start.record(stream)
+        ex.launch_device([dx.ptr], [dout.ptr], stream.handle)
+        end.record(stream)
         stream.synchronize()
-        assert_rel(dout.cpu().numpy(), ref, 1e-5)
+        assert start.elapsed_ms(end) >= 0.0
+        assert_rel(dout.download(np.zeros(64, np.float32)), ref, 1e-5)
+        ex.set_profiling(True)
+        ex.launch_device([dx.ptr], [dout.ptr], stream.handle)
+        ks = ex.kernels()
+        assert len(ks) == 1 and ks[0].klass == "row" and ks[0].last_ms > 0
+        for b in (dx, dout):
+            b.free()
+        stream.destroy()
 
 
 def test_bad_wire_is_refused_by_compile():

@@ -5,6 +5,11 @@
 // requires (src/eval/root.zig:10-16).
 #pragma once
 #pragma clang fp contract(off)
+#ifndef __HIPCC_RTC__
+// hiprtc provides the HIP device environment itself; an offline hipcc build (the build-time check of
+// these sources) needs the header.
+#include <hip/hip_runtime.h>
+#endif
 
 typedef signed char i8_t;
 typedef short i16_t;
@@ -34,6 +39,63 @@ template <typename T, typename I> __device__ __forceinline__ T ld(const T* __res
 template <typename T, typename I> __device__ __forceinline__ void st(T* __restrict__ p, I i, T v) { p[i] = v; }
 template <typename I> __device__ __forceinline__ bool ld_i1(const u8_t* __restrict__ p, I i) { return p[i] != 0; }
 template <typename I> __device__ __forceinline__ void st_i1(u8_t* __restrict__ p, I i, bool v) { p[i] = v ? 1 : 0; }
+
+// ---- f32 transcendentals used by generated kernels ----
+// exp: e^x = 2^(x log2 e). The product x * log2(e) is carried as eh + el, with el the exact rounding
+// error of the f32 product (one FMA) plus x times the tail of log2(e); n = rint(eh) is clamped to
+// [-160, 160] so that +-inf and NaN propagate through the same instructions; 2^f for |f| <= 0.5 comes
+// from the hardware exp2 (v_exp_f32, 1 ulp) and 2^n from ldexp. About 1.5 ulp over the f32 range,
+// with no compares (so no VCC hazard wait states). el is clamped to [-1, 1]: it is NaN only for
+// infinite x, where the clamp turns it into a finite value and eh alone gives 0 or inf.
+__device__ __forceinline__ float exp_f32(float x) {
+  const float L2E = 0x1.715476p+0f, L2E_LO = 0x1.4ae0cp-26f;
+  const float eh = x * L2E;
+  const float el = __builtin_fminf(__builtin_fmaxf(__builtin_fmaf(x, L2E_LO, __builtin_fmaf(x, L2E, -eh)), -1.0f), 1.0f);
+  const float n = __builtin_rintf(__builtin_fminf(__builtin_fmaxf(eh, -160.0f), 160.0f));
+  const float f = (eh - n) + el;
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
+}
+
+// sin / cos: Cody-Waite reduction by pi/2 with a three-part constant (P1 + P2 + P3 = pi/2 to ~2^-75;
+// the first FMA is exact for the quadrants below 2^17), then Taylor polynomials for sin and cos on
+// [-pi/4, pi/4] (truncation below 2^-28). Arguments of magnitude 2^17 and beyond take the library's
+// sinf / cosf (Payne-Hanek reduction).
+__device__ __forceinline__ float sincos_core(float r, int q) {
+  const float r2 = r * r;
+  float s = __builtin_fmaf(r2, 0x1.71de3ap-19f, -0x1.a01a02p-13f);  // 1/9!, -1/7!
+  s = __builtin_fmaf(r2, s, 0x1.111112p-7f);                          // 1/5!
+  s = __builtin_fmaf(r2, s, -0x1.555556p-3f);                         // -1/3!
+  s = __builtin_fmaf(r * r2, s, r);
+  float c = __builtin_fmaf(r2, -0x1.27e4fcp-22f, 0x1.a01a02p-16f);  // -1/10!, 1/8!
+  c = __builtin_fmaf(r2, c, -0x1.6c16c2p-10f);                        // -1/6!
+  c = __builtin_fmaf(r2, c, 0x1.555556p-5f);                          // 1/4!
+  c = __builtin_fmaf(r2, c, -0.5f);
+  c = __builtin_fmaf(r2, c, 1.0f);
+  const float v = (q & 1) ? c : s;
+  return __builtin_bit_cast(float, __builtin_bit_cast(u32_t, v) ^ ((u32_t)(q & 2) << 30));
+}
+
+__device__ __forceinline__ float sin_f32(float x) {
+  const float P1 = 0x1.921fb6p+0f, P2 = -0x1.777a5cp-25f, P3 = -0x1.ee59dap-50f;
+  const float k = __builtin_rintf(x * 0x1.45f306p-1f);
+  float r = __builtin_fmaf(-k, P1, x);
+  r = __builtin_fmaf(-k, P2, r);
+  r = __builtin_fmaf(-k, P3, r);
+  float v = sincos_core(r, (int)k);
+  if (__builtin_fabsf(x) >= 0x1p+17f) v = sinf(x);
+  return v;
+}
+
+__device__ __forceinline__ float cos_f32(float x) {
+  const float P1 = 0x1.921fb6p+0f, P2 = -0x1.777a5cp-25f, P3 = -0x1.ee59dap-50f;
+  const float k = __builtin_rintf(x * 0x1.45f306p-1f);
+  float r = __builtin_fmaf(-k, P1, x);
+  r = __builtin_fmaf(-k, P2, r);
+  r = __builtin_fmaf(-k, P3, r);
+  float v = sincos_core(r, (int)k + 1);
+  if (__builtin_fabsf(x) >= 0x1p+17f) v = cosf(x);
+  return v;
+}
 
 // ---- integer arithmetic wraps at the declared width; division by zero yields zero ----
 template <typename T, typename U> __device__ __forceinline__ T wadd(T a, T b) { return (T)((U)a + (U)b); }

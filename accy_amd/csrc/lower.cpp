@@ -195,6 +195,16 @@ std::string KernelWriter::load(int slot, const std::string& off, DType d) {
   }
 }
 
+std::string KernelWriter::load_at(int slot, const std::string& base, const std::string& idx, DType d) {
+  std::string p = "(" + arg(slot, false) + " + " + base + ")";
+  switch (d) {
+    case DType::f16: return "accy::ld_f16(" + p + ", " + idx + ")";
+    case DType::bf16: return "accy::ld_bf16(" + p + ", " + idx + ")";
+    case DType::i1: return "accy::ld_i1(" + p + ", " + idx + ")";
+    default: return p + "[" + idx + "]";
+  }
+}
+
 std::string KernelWriter::store(int slot, const std::string& off, DType d, const std::string& v) {
   std::string a = arg(slot, true);
   switch (d) {
@@ -254,12 +264,12 @@ std::string KernelWriter::value(uint32_t vid, const std::vector<std::string>& co
         switch (u) {
           case Unary::neg: e = "-" + x; break;
           case Unary::abs: e = (f ? "fabsf(" : "fabs(") + x + ")"; break;
-          case Unary::exp: e = (f ? "expf(" : "exp(") + x + ")"; break;
+          case Unary::exp: e = (f ? "accy::exp_f32(" : "exp(") + x + ")"; break;
           case Unary::log: e = (f ? "logf(" : "log(") + x + ")"; break;
           case Unary::sqrt: e = (f ? "sqrtf(" : "sqrt(") + x + ")"; break;
           case Unary::tanh: e = (f ? "tanhf(" : "tanh(") + x + ")"; break;
-          case Unary::sin: e = (f ? "sinf(" : "sin(") + x + ")"; break;
-          case Unary::cos: e = (f ? "cosf(" : "cos(") + x + ")"; break;
+          case Unary::sin: e = (f ? "accy::sin_f32(" : "sin(") + x + ")"; break;
+          case Unary::cos: e = (f ? "accy::cos_f32(" : "cos(") + x + ")"; break;
           case Unary::tan: e = (f ? "tanf(" : "tan(") + x + ")"; break;
         }
         return emit(round_to(d, e));

@@ -61,6 +61,8 @@ class KernelWriter {
   std::string value(uint32_t vid, const std::vector<std::string>& coords, Scope& sc);
   std::string arg(int slot, bool write);
   std::string load(int slot, const std::string& off, DType d);
+  // Load of element `idx` past `base` (pointer-base form, so adjacent idx merge into vector loads).
+  std::string load_at(int slot, const std::string& base, const std::string& idx, DType d);
   std::string store(int slot, const std::string& off, DType d, const std::string& v);
   std::string tmp();
   std::string params() const;

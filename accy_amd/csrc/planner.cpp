@@ -103,6 +103,7 @@ class Planner {
         needed_[v] = true;
       }
     }
+    mark_gemm_operands();
     for (uint32_t v = 0; v < n; ++v) {
       if (!live_[v] || done_[v]) continue;
       const Op& op = g_.ops[v];
@@ -111,7 +112,7 @@ class Planner {
         case Kind::reduce:
           if (!row_group(v)) fold(v);
           break;
-        case Kind::dot_general: dot_serial(v); break;
+        case Kind::dot_general: dot(v); break;
         case Kind::scatter_add: scatter_add(v); break;
         case Kind::scan: case Kind::projection: case Kind::custom_call: case Kind::sparse_cross_entropy:
           fail(Err::Unsupported, std::string(kind_name(op.kind)) + " is not supported by the HIP target");
@@ -403,6 +404,32 @@ class Planner {
       }
     }
     std::map<std::string, std::set<int>> use_record;
+    // A load whose offset is `rest + c` (c the row's element index, rank-1 row) is written as
+    // (ptr + rest + c0)[u] so that the VEC adjacent loads of one thread merge into one vector load.
+    auto direct_load = [&](int slot, const std::string& off, DType d) -> std::string {
+      if (VEC == 1 || tc.size() != 1 || tc[0] != "c" || off.size() < 2 || off.front() != '(' || off.back() != ')')
+        return w.load(slot, off, d);
+      std::string body = off.substr(1, off.size() - 2), rest;
+      bool found = false;
+      size_t pos = 0;
+      while (pos <= body.size()) {
+        size_t nx = body.find(" + ", pos);
+        std::string term = body.substr(pos, nx == std::string::npos ? std::string::npos : nx - pos);
+        bool has_c = false;
+        for (size_t i = 0; i < term.size(); ++i) {
+          bool ident_start = i == 0 || !(isalnum((unsigned char)term[i - 1]) || term[i - 1] == '_');
+          bool ident_end = i + 1 == term.size() || !(isalnum((unsigned char)term[i + 1]) || term[i + 1] == '_');
+          if (term[i] == 'c' && ident_start && ident_end) has_c = true;
+        }
+        if (term == "c" && !found) found = true;
+        else if (has_c) return w.load(slot, off, d);
+        else rest += (rest.empty() ? "" : " + ") + term;
+        if (nx == std::string::npos) break;
+        pos = nx + 3;
+      }
+      if (!found) return w.load(slot, off, d);
+      return w.load_at(slot, "(" + (rest.empty() ? std::string("0") : rest) + ") + c0", "u", d);
+    };
     w.leaf_hook = [&](int slot, const std::string& off, DType d, Scope& sc, std::string& out) -> bool {
       bool varies = false;
       for (const auto& t : tc)
@@ -411,10 +438,15 @@ class Planner {
       std::string key = std::to_string(slot) + "|" + off;
       use_record[key].insert(cur_pass);
       auto it = leaf_array.find(key);
-      if (it == leaf_array.end()) return false;
+      if (it == leaf_array.end()) {
+        std::string t = w.tmp();
+        sc.out << sc.indent << "const " << compute_type(d) << " " << t << " = " << direct_load(slot, off, d) << ";\n";
+        out = t;
+        return true;
+      }
       std::string elem = it->second + "[e * " + std::to_string(VEC) + " + u]";
       if (leaf_first[key] == cur_pass) {
-        sc.out << sc.indent << elem << " = " << w.load(slot, off, d) << ";\n";
+        sc.out << sc.indent << elem << " = " << direct_load(slot, off, d) << ";\n";
         if (declared.insert(key).second)
           decls += "    " + std::string(compute_type(d)) + " " + it->second + "[" + std::to_string(E * VEC) + "];\n";
       }
@@ -438,10 +470,11 @@ class Planner {
     std::string loop_head;
     {
       std::ostringstream lh;
-      lh << (unrolled ? "#pragma unroll\n" : "#pragma unroll 1\n") << "    for (int e = 0; e < " << E << "; ++e) {\n"
+      lh << (unrolled ? "#pragma unroll\n" : "#pragma unroll 2\n") << "    for (int e = 0; e < " << E << "; ++e) {\n"
+         << "      const I c0 = ((I)e * " << B << " + (I)threadIdx.x) * " << VEC << ";\n"
          << "#pragma unroll\n"
          << "      for (int u = 0; u < " << VEC << "; ++u) {\n"
-         << "        const I c = ((I)e * " << B << " + (I)threadIdx.x) * " << VEC << " + u;\n";
+         << "        const I c = c0 + u;\n";
       if (guard) lh << "        if (c < (I)" << tn << ") {\n";
       loop_head = lh.str();
     }
@@ -511,6 +544,205 @@ class Planner {
   }
 
   std::map<std::string, std::set<int>> probe_use_;
+
+  // ---- strided views: a value that is a transpose / rename / broadcast of a buffer ----
+  struct View {
+    int slot = -1;
+    int64_t offset = 0;
+    std::vector<int64_t> strides;  // per dim of the viewed value, in elements
+  };
+
+  bool resolve_view(uint32_t v, View& out) const {
+    int s = slots_.available(v);
+    const Op& op = g_.ops[v];
+    const Type& t = op.result;
+    if (s >= 0) {
+      out.slot = s;
+      out.offset = 0;
+      out.strides = row_major_strides(t.dims);
+      return true;
+    }
+    View in;
+    switch (op.kind) {
+      case Kind::transpose:
+        if (!resolve_view(op.args[0], in)) return false;
+        out = in;
+        for (size_t k = 0; k < t.rank(); ++k) out.strides[k] = in.strides[(size_t)op.ints[k]];
+        return true;
+      case Kind::reshape: {
+        const Type& it = g_.type(op.args[0]);
+        if (it.rank() != t.rank()) return false;
+        for (size_t k = 0; k < t.rank(); ++k)
+          if (it.dims[k].extent != t.dims[k].extent) return false;
+        return resolve_view(op.args[0], out);
+      }
+      case Kind::broadcast_in_dim: {
+        if (!resolve_view(op.args[0], in)) return false;
+        const Type& it = g_.type(op.args[0]);
+        out.slot = in.slot;
+        out.offset = in.offset;
+        out.strides.assign(t.rank(), 0);
+        for (size_t j = 0; j < op.ints.size(); ++j)
+          if (it.dims[j].extent != 1) out.strides[(size_t)op.ints[j]] = in.strides[j];
+        return true;
+      }
+      default:
+        return false;
+    }
+  }
+
+  // Collapses a group of dims (in the given order) into one extent and stride, if the group is
+  // contiguous in the view; an empty group is extent 1, stride 0.
+  static bool flatten(const std::vector<Dim>& dims, const std::vector<int64_t>& strides,
+                      const std::vector<size_t>& group, int64_t& extent, int64_t& stride) {
+    extent = 1;
+    stride = 0;
+    bool first = true;
+    for (size_t gi = group.size(); gi-- > 0;) {
+      size_t d = group[gi];
+      int64_t e = dims[d].extent;
+      if (e == 1) continue;
+      if (first) {
+        stride = strides[d];
+        first = false;
+      } else if (strides[d] != stride * extent) {
+        return false;
+      }
+      extent *= e;
+    }
+    return true;
+  }
+
+  struct GemmShape {
+    int64_t batch = 1, m = 1, n = 1, k = 1;
+    int64_t a_b = 0, a_m = 0, a_k = 0, b_b = 0, b_k = 0, b_n = 0;
+    View a, b;
+  };
+
+  bool gemm_shape(const Op& op, GemmShape& gs) const {
+    const Type& L = g_.type(op.args[0]);
+    const Type& R = g_.type(op.args[1]);
+    if (!resolve_view(op.args[0], gs.a) || !resolve_view(op.args[1], gs.b)) return false;
+    auto in = [](const std::vector<int64_t>& a, size_t d) { return std::find(a.begin(), a.end(), (int64_t)d) != a.end(); };
+    std::vector<size_t> lb(op.lhs_batch.begin(), op.lhs_batch.end()), rb(op.rhs_batch.begin(), op.rhs_batch.end());
+    std::vector<size_t> lc(op.lhs_contract.begin(), op.lhs_contract.end()),
+        rc(op.rhs_contract.begin(), op.rhs_contract.end());
+    std::vector<size_t> lf, rf;
+    for (size_t i = 0; i < L.rank(); ++i)
+      if (!in(op.lhs_contract, i) && !in(op.lhs_batch, i)) lf.push_back(i);
+    for (size_t i = 0; i < R.rank(); ++i)
+      if (!in(op.rhs_contract, i) && !in(op.rhs_batch, i)) rf.push_back(i);
+    int64_t e2;
+    if (!flatten(L.dims, gs.a.strides, lb, gs.batch, gs.a_b)) return false;
+    if (!flatten(R.dims, gs.b.strides, rb, e2, gs.b_b) || e2 != gs.batch) return false;
+    if (!flatten(L.dims, gs.a.strides, lf, gs.m, gs.a_m)) return false;
+    if (!flatten(R.dims, gs.b.strides, rf, gs.n, gs.b_n)) return false;
+    if (!flatten(L.dims, gs.a.strides, lc, gs.k, gs.a_k)) return false;
+    if (!flatten(R.dims, gs.b.strides, rc, e2, gs.b_k) || e2 != gs.k) return false;
+    // Contraction axes must flatten in the same order on both sides: check pairwise extents.
+    for (size_t i = 0; i < lc.size(); ++i)
+      if (L.dims[lc[i]].extent != R.dims[rc[i]].extent) return false;
+    return true;
+  }
+
+  // The MFMA template takes 16-bit operands whose K or M/N stride is 1, with 8-element aligned rows.
+  bool gemm_eligible(const Op& op, GemmShape& gs) const {
+    if (!opt_.allow_gemm) return false;
+    DType d = op.result.dtype;
+    if (d != DType::bf16 && d != DType::f16) return false;
+    if (!gemm_shape(op, gs)) return false;
+    if (gs.m * gs.n * gs.k == 0) return false;
+    auto ok8 = [](int64_t v) { return v % 8 == 0; };
+    bool a_kc = gs.a_k == 1 && ok8(gs.k) && (gs.m == 1 || ok8(gs.a_m));
+    bool a_mc = gs.a_m == 1 && ok8(gs.m) && (gs.k == 1 || ok8(gs.a_k));
+    bool b_kc = gs.b_k == 1 && ok8(gs.k) && (gs.n == 1 || ok8(gs.b_n));
+    bool b_nc = gs.b_n == 1 && ok8(gs.n) && (gs.k == 1 || ok8(gs.b_k));
+    if (!(a_kc || a_mc) || !(b_kc || b_nc)) return false;
+    if (!ok8(gs.a_b) || !ok8(gs.b_b) || !ok8(gs.a.offset) || !ok8(gs.b.offset)) return false;
+    return true;
+  }
+
+  // Marks dot operands that are not plain views of a buffer: they are materialised first (by the
+  // kernel that produces them, e.g. as a full-row output of a row kernel).
+  void mark_gemm_operands() {
+    for (uint32_t v = 0; v < g_.ops.size(); ++v) {
+      const Op& op = g_.ops[v];
+      if (!live_[v] || op.kind != Kind::dot_general) continue;
+      if (op.result.dtype != DType::bf16 && op.result.dtype != DType::f16) continue;
+      for (uint32_t a : op.args) {
+        if (!view_chain_to_anchor(a)) needed_[a] = true;
+      }
+    }
+  }
+
+  // True when `v` is a (transpose / rename / broadcast) view of a parameter or an anchor value.
+  bool view_chain_to_anchor(uint32_t v) const {
+    const Op& op = g_.ops[v];
+    switch (op.kind) {
+      case Kind::transpose: case Kind::broadcast_in_dim: return view_chain_to_anchor(op.args[0]);
+      case Kind::reshape: {
+        const Type& it = g_.type(op.args[0]);
+        if (it.rank() != op.result.rank()) return false;
+        for (size_t k = 0; k < it.rank(); ++k)
+          if (it.dims[k].extent != op.result.dims[k].extent) return false;
+        return view_chain_to_anchor(op.args[0]);
+      }
+      case Kind::parameter: case Kind::dot_general: case Kind::reduce: case Kind::scatter_add: return true;
+      default: return needed_[v];
+    }
+  }
+
+  void dot(uint32_t v) {
+    const Op& op = g_.ops[v];
+    GemmShape gs;
+    if (gemm_eligible(op, gs)) {
+      gemm(v, gs);
+      return;
+    }
+    dot_serial(v);
+  }
+
+  void gemm(uint32_t v, const GemmShape& gs) {
+    const Op& op = g_.ops[v];
+    int out = slots_.slot_of[v] >= 0 ? slots_.slot_of[v] : temp_slot(v);
+    DType d = op.result.dtype;
+    const int BM = 256, BN = 256, BK = 64, WM = 4, WN = 2;
+    KernelWriter w(g_, slots_, "i64_t");
+    std::string a = w.arg(gs.a.slot, false), b = w.arg(gs.b.slot, false), c = w.arg(out, true);
+    std::string nm = name("gemm", v);
+    std::ostringstream src;
+    src << "#include \"gemm\"\n";
+    src << "struct Cfg_" << nm << " {\n"
+        << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
+        << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
+        << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", A_K = " << gs.a_k << ";\n"
+        << "  static constexpr long B_B = " << gs.b_b << ", B_K = " << gs.b_k << ", B_N = " << gs.b_n << ";\n"
+        << "  static constexpr bool A_KC = " << (gs.a_k == 1 ? "true" : "false")
+        << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n"
+        << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
+        << ", WAVES_N = " << WN << ";\n};\n";
+    src << "struct Epi_" << nm << " {\n  u16_t* __restrict__ c;\n"
+        << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
+        << "    c[b * " << gs.m * gs.n << "L + m * " << gs.n << "L + n] = accy::f32_to_"
+        << (d == DType::bf16 ? "bf16" : "f16") << "(v);\n  }\n};\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << WM * WN * 64 << ") " << nm << "(const u16_t* __restrict__ "
+        << a << ", const u16_t* __restrict__ " << b << ", u16_t* __restrict__ " << c << ") {\n"
+        << "  accy::gemm::mma16<Cfg_" << nm << ">(" << a << " + " << gs.a.offset << "L, " << b << " + "
+        << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
+    KernelStep k;
+    k.source = src.str();
+    k.name = nm;
+    int64_t tiles = ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
+    k.grid[0] = (uint32_t)tiles;
+    k.grid[1] = (uint32_t)gs.batch;
+    k.block[0] = WM * WN * 64;
+    k.shared_bytes = 2u * (BM + BN) * (BK + 8) * 2u;
+    k.klass = "gemm";
+    k.label = "gemm:%" + std::to_string(v);
+    k.algorithmic_flops = 2.0 * (double)gs.batch * (double)gs.m * (double)gs.n * (double)gs.k;
+    push(std::move(k), w);
+    finish(v);
+  }
 
   // ---- dot_general with runCpu's per-output serial k order ----
   void dot_serial(uint32_t v) {

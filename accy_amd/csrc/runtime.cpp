@@ -12,6 +12,8 @@
 namespace accy {
 
 extern const char* const kCommonDeviceSource;
+extern const char* const kGemmDeviceSource;
+extern const char* const kAttentionDeviceSource;
 
 namespace {
 
@@ -50,8 +52,18 @@ hipFunction_t load_kernel(const std::string& body, const std::string& name) {
 
 }  // namespace
 
+// Generated kernels name the hand-written templates they instantiate with `#include "<name>"`; the
+// template text (embedded in this library) replaces that line.
 std::string full_kernel_source(const std::string& body) {
-  return std::string(kCommonDeviceSource) + "\n" + body;
+  std::string out = std::string(kCommonDeviceSource) + "\n";
+  const std::pair<const char*, const char*> templates[] = {{"#include \"gemm\"\n", kGemmDeviceSource},
+                                                           {"#include \"attention\"\n", kAttentionDeviceSource}};
+  std::string rest = body;
+  for (const auto& t : templates) {
+    size_t p = rest.find(t.first);
+    if (p != std::string::npos) rest.replace(p, std::strlen(t.first), std::string(t.second) + "\n");
+  }
+  return out + rest;
 }
 
 std::vector<char> compile_kernel_source(const std::string& source, const std::string& name) {
@@ -108,9 +120,15 @@ Executor::Executor(Program program, Plan plan) : program_(std::move(program)), p
         check(hipMemcpy(owned_[i], s.data.data(), s.bytes, hipMemcpyHostToDevice), "hipMemcpy");
     }
     fn_.assign(plan_.steps.size(), nullptr);
+    int dev = 0, max_lds = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    check(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
     for (size_t i = 0; i < plan_.steps.size(); ++i) {
       const Step& st = plan_.steps[i];
       if (st.type != Step::Kernel) continue;
+      if ((int)st.kernel.shared_bytes > max_lds)
+        throw HipFailure(kStatusCompileFailed, st.kernel.label + " needs " + std::to_string(st.kernel.shared_bytes) +
+                                                   " bytes of LDS; the device allows " + std::to_string(max_lds));
       fn_[i] = load_kernel(st.kernel.source, st.kernel.name);
       KernelTiming t;
       t.label = st.kernel.label;

@@ -144,6 +144,51 @@ def test_small_attention_and_decoder():
     assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16")
 
 
+# ---- contractions on the MFMA template ----
+
+def _qk_program(heads, q, kk, d, dtype):
+    return T.define("qk", [T.spec(dtype, head=heads, query=q, dim=d), T.spec(dtype, head=heads, key=kk, dim=d)],
+                    lambda b, a: a[0].contract(a[1], "dim"))
+
+
+@pytest.mark.parametrize("m,k,n,dtype", [(256, 256, 256, "bf16"), (300, 200, 136, "bf16"), (8, 64, 1000, "f16"),
+                                         (520, 1032, 264, "f16"), (1, 8, 8, "bf16")])
+def test_gemm_mfma_nn(m, k, n, dtype):
+    say(f"gemm nn {m}x{k}x{n} {dtype}")
+    prog = W.gemm_program(m, k, n, dtype)
+    assert "accy_gemm" in hip.plan_source(prog)
+    ins = W.gemm_inputs(m, k, n, dtype, seed=m + n)
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_gemm_mfma_batched_nt(dtype):
+    prog = _qk_program(3, 200, 264, 64, dtype)
+    assert "accy_gemm" in hip.plan_source(prog)
+    ins = [W.to_dtype(W.normal(21, 3 * 200 * 64), dtype).reshape(3, 200, 64),
+           W.to_dtype(W.normal(22, 3 * 264 * 64), dtype).reshape(3, 264, 64)]
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype)
+
+
+def test_gemm_mfma_transposed_lhs():
+    # A stored [k, m]: the contraction canonicalises it with a transpose, an M-contiguous operand.
+    prog = T.define("tn", [T.spec("bf16", k=128, m=96), T.spec("bf16", k=128, n=64)],
+                    lambda b, a: a[0].contract(a[1], "k"))
+    assert "accy_gemm" in hip.plan_source(prog)
+    ins = [W.to_dtype(W.uniform(23, 128 * 96, -1, 1), "bf16").reshape(128, 96),
+           W.to_dtype(W.uniform(24, 128 * 64, -1, 1), "bf16").reshape(128, 64)]
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16")
+
+
+def test_gemm_bf16_full_size_on_sampled_rows():
+    say("gemm bf16 8192^3 (full)")
+    a, b = W.gemm_inputs(8192, 8192, 8192, "bf16")
+    got = hip_run(W.gemm_program(8192, 8192, 8192, "bf16"), [a, b])[0]
+    rows = np.sort(np.random.default_rng(1).choice(8192, 16, replace=False))
+    ref = oracle_run(W.gemm_program(16, 8192, 8192, "bf16"), [a[rows], b])[0]
+    assert_normwise(got[rows], ref, 2e-2, "bf16")
+
+
 # ---- exact classes ----
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])

@@ -74,6 +74,17 @@ def config_table():
             sample=lambda: (W.attention_program(1, 1024, 128, "f16"), W.attention_inputs(1, 1024, 128, "f16"),
                             4.0 * 1 * 1024 * 1024 * 128),
             sample_desc="1 head x 1024 queries x 1024 keys", workload=dict(heads=32, seq=4096, dim=128)),
+        # Not a measured config: a plain copy of 1 GiB (y = x * 1), whose HBM counters calibrate the
+        # FETCH_SIZE / WRITE_SIZE readings of the other kernels.
+        "calib-copy": dict(
+            make=lambda: (T.define("copy", [T.spec("f32", row=32768, feature=8192)],
+                                   lambda b, a: a[0].mul(b.full_float(T.Type("f32", ()), 1.0))),
+                          W.logsumexp_inputs(32768, 8192, seed=2)),
+            dtype="f32", unit="GB/s", bound="hbm", work=2 * 32768 * 8192 * 4, peak=HBM_PEAK_GBS,
+            sample=lambda: (T.define("copy", [T.spec("f32", row=1024, feature=8192)],
+                                     lambda b, a: a[0].mul(b.full_float(T.Type("f32", ()), 1.0))),
+                            W.logsumexp_inputs(1024, 8192, seed=2), 2 * 1024 * 8192 * 4),
+            sample_desc="1024 rows", workload=dict(rows=32768, features=8192)),
         "c5-decoder": dict(
             make=lambda: (W.decoder_program(), W.decoder_inputs()),
             dtype="bf16", unit="TFLOP/s", bound="mfma", work=893353197568.0, peak=MFMA_PEAK_TFLOPS["bf16"],

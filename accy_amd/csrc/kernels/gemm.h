@@ -9,7 +9,10 @@
 //
 // Operand layouts: an operand whose K stride is 1 is loaded as 16-byte vectors along K and written
 // to LDS unchanged; an operand whose M (or N) stride is 1 is loaded as 8 x 8 blocks (8 vectors along
-// M/N at 8 consecutive k) and transposed in registers before the LDS write. Blocks are renumbered so
+// M/N at 8 consecutive k) and transposed in registers before the LDS write. Neighbouring lanes take
+// neighbouring k-groups of one row group, so the 8 lanes of one LDS store cycle write 8 different
+// 16-byte columns of the padded rows (distinct banks) while each global load instruction still covers
+// whole 128-byte lines (8 lanes x 16 bytes of one k row). Blocks are renumbered so
 // that the tiles dispatched to one XCD are neighbours (shared A rows / B columns in that XCD's L2).
 //
 // The configuration struct C supplies extents, strides (elements), tile shape and dtype; the
@@ -89,10 +92,11 @@ struct TileLoader {
       }
     } else {
       constexpr int RG = ROWS / 8;
+      (void)RG;
 #pragma unroll
       for (int b = 0; b < PER_THREAD / 8; ++b) {
         const int bidx = t + b * THREADS;
-        const int kg = bidx / RG, rg = bidx % RG;
+        const int kg = bidx % (BK / 8), rg = bidx / (BK / 8);
         const long r = r0 + rg * 8;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -118,10 +122,11 @@ struct TileLoader {
       }
     } else {
       constexpr int RG = ROWS / 8;
+      (void)RG;
 #pragma unroll
       for (int b = 0; b < PER_THREAD / 8; ++b) {
         const int bidx = t + b * THREADS;
-        const int kg = bidx / RG, rg = bidx % RG;
+        const int kg = bidx % (BK / 8), rg = bidx / (BK / 8);
         u32x4 in[8], out[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) in[i] = v[b * 8 + i];
@@ -219,6 +224,174 @@ __device__ __forceinline__ void mma16(const u16_t* __restrict__ A, const u16_t* 
           const long m = row_base + i * 32 + g * 8 + r, n = col_base + j * 32;
           if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) epi(batch, m, n, acc[i][j][g * 4 + r]);
         }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Direct-to-LDS pipeline (tiles that divide the problem exactly).
+//
+// Each K step (BK = 32) stages a BM x 32 tile of A and a 32 x BN tile of B straight from global
+// memory into LDS with global_load_lds_dwordx4 (lane l of an instruction writes bytes [16 l, 16 l + 16)
+// after the wave's LDS base), four stages deep in four distinct LDS arrays, so that 3 K steps of loads
+// are in flight under the MFMAs. Each wave waits only for its own loads of the step it consumes
+// (s_waitcnt vmcnt), then one s_barrier (no memory fence) publishes every wave's part.
+//
+// LDS layouts (both conflict-free for the fragment reads of 8 / 16 consecutive lanes):
+//  * K-contiguous operand (rows = M or N, 64 bytes of K per row): 128-byte lines of two rows; the
+//    16-byte chunk at slot s of line L holds logical slot s ^ (L & 7). Fragments: ds_read_b128.
+//  * M/N-contiguous operand (rows = K, BN x 2 bytes per row): the 32-byte unit at position p of row k
+//    holds logical unit p ^ (k & 7). Fragments: ds_read_b64_tr_b16, which hands lane i of each
+//    16-lane group element (i mod 4) of the 8 bytes addressed by lane 4t + i / 4 as its element t;
+//    pointing lane j of the group at row k0 + j / 4, columns n0 + 4 (j mod 4) .. + 3 gives lane i the
+//    4 values B[k0 .. k0 + 3][n0 + i], the MFMA B-operand layout (and likewise for A).
+// ---------------------------------------------------------------------------------------------
+
+#define ACCY_LDS __attribute__((address_space(3)))
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void dma16(const void* g, ACCY_LDS void* l) { __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0); }
+
+template <int N> __device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Issues this wave's share of one operand tile. KC: rows of 32 k (64 bytes); else rows of k.
+template <int ROWS, bool KC, long SR, long SK>
+__device__ __forceinline__ void dma_tile(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave, int lane) {
+  constexpr int INSTRS = ROWS * 64 / 1024;  // 1 KiB per wave instruction
+  static_assert(INSTRS % 4 == 0, "four waves share the tile");
+#pragma unroll
+  for (int i = 0; i < INSTRS / 4; ++i) {
+    const int gi = wave * (INSTRS / 4) + i;
+    const u16_t* src;
+    if constexpr (KC) {
+      const int q = (lane & 7) ^ (lane >> 3);  // logical slot of this lane's physical chunk
+      const int row = 16 * gi + 2 * (lane >> 3) + (q >> 2);
+      src = base + (r0 + row) * SR + k0 + 8 * (q & 3);
+    } else {
+      constexpr int ROWB = ROWS * 2;                // bytes per k row
+      constexpr int LPR = ROWB / 16;                // lanes per k row
+      constexpr int RPI = 1024 / ROWB;              // k rows per instruction
+      const int row = RPI * gi + lane / LPR;
+      const int p = lane % LPR;
+      const int u = (p >> 1) ^ (row & 7);
+      src = base + (k0 + row) * SK + r0 + 16 * u + 8 * (p & 1);
+    }
+    dma16(src, (ACCY_LDS void*)(lds + gi * 512));
+  }
+}
+
+// Fragment of 32 rows (M or N) x 16 k for one MFMA, read from a stage.
+template <int ROWS, bool KC>
+__device__ __forceinline__ u32x4 frag(const u16_t* lds, int row0, int s, int lane) {
+  if constexpr (KC) {
+    const int r = row0 + (lane & 31), c = 2 * s + (lane >> 5);
+    const int line = r >> 1, slot = ((r & 1) << 2) | c;
+    return *(const u32x4*)(lds + line * 64 + ((slot ^ (line & 7)) << 3));
+  } else {
+    constexpr int ROWE = ROWS;  // elements per k row
+    const int g = lane >> 4, i = lane & 15;
+    const int n0 = row0 + ((g & 1) << 4);
+    u32x4 out;
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int k = 16 * s + 8 * (g >> 1) + 4 * rr + (i >> 2);
+      const int unit = (n0 >> 4) ^ (k & 7);
+      const u16_t* p = lds + k * ROWE + unit * 16 + 4 * (i & 3);
+      const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ACCY_LDS i16x4*)p);
+      const u32_t lo = (u32_t)(u16_t)v[0] | ((u32_t)(u16_t)v[1] << 16);
+      const u32_t hi = (u32_t)(u16_t)v[2] | ((u32_t)(u16_t)v[3] << 16);
+      out[2 * rr] = lo;
+      out[2 * rr + 1] = hi;
+    }
+    return out;
+  }
+}
+
+template <class C, int STAGE, int NEXT, int WAIT>
+struct DmaStep {
+  template <class Acc>
+  __device__ __forceinline__ static void run(const u16_t* __restrict__ Ab, const u16_t* __restrict__ Bb, long m0,
+                                             long n0, long kt, bool issue, u16_t* const (&as)[4],
+                                             u16_t* const (&bs)[4], Acc& acc, int wave, int lane, int wm, int wn) {
+    constexpr int BM = C::BM, BN = C::BN;
+    constexpr int TM = BM / 64, TN = BN / 64;
+    wait_vmcnt<WAIT>();
+    __builtin_amdgcn_s_barrier();
+    if (issue) {
+      dma_tile<BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, (kt + 3) * 32, as[NEXT], wave, lane);
+      dma_tile<BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, (kt + 3) * 32, bs[NEXT], wave, lane);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = frag<BM, C::A_KC>(as[STAGE], wm * (BM / 2) + i * 32, s, lane);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = frag<BN, C::B_KC>(bs[STAGE], wn * (BN / 2) + j * 32, s, lane);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<C::DT>(a[i], b[j], acc[i][j]);
+    }
+  }
+};
+
+// Requires M % BM == 0, N % BN == 0, K % 128 == 0, 16-byte aligned rows; 256 threads (2 x 2 waves).
+template <class C, class Epi>
+__device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi) {
+  constexpr int BM = C::BM, BN = C::BN;
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr long TILES_M = C::M / BM, TILES_N = C::N / BN, KT = C::K / 32;
+  static_assert(C::M % BM == 0 && C::N % BN == 0 && C::K % 128 == 0, "exact tiles only");
+  constexpr int PER = (BM * 64 / 1024) / 4 + (BN * 64 / 1024) / 4;  // DMA instructions per wave per step
+  __shared__ __attribute__((aligned(1024))) u16_t a0[BM * 32], a1[BM * 32], a2[BM * 32], a3[BM * 32];
+  __shared__ __attribute__((aligned(1024))) u16_t b0[BN * 32], b1[BN * 32], b2[BN * 32], b3[BN * 32];
+  u16_t* const as[4] = {a0, a1, a2, a3};
+  u16_t* const bs[4] = {b0, b1, b2, b3};
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  long tm, tn;
+  tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
+  const long m0 = tm * BM, n0 = tn * BN, batch = blockIdx.y;
+  const u16_t* __restrict__ Ab = A + batch * C::A_B;
+  const u16_t* __restrict__ Bb = B + batch * C::B_B;
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
+
+#pragma unroll
+  for (int s = 0; s < 3; ++s) {
+    dma_tile<BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, s * 32, as[s], wave, lane);
+    dma_tile<BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, s * 32, bs[s], wave, lane);
+  }
+  long kt = 0;
+  for (; kt + 4 < KT; kt += 4) {
+    DmaStep<C, 0, 3, 2 * PER>::run(Ab, Bb, m0, n0, kt, true, as, bs, acc, wave, lane, wm, wn);
+    DmaStep<C, 1, 0, 2 * PER>::run(Ab, Bb, m0, n0, kt + 1, true, as, bs, acc, wave, lane, wm, wn);
+    DmaStep<C, 2, 1, 2 * PER>::run(Ab, Bb, m0, n0, kt + 2, true, as, bs, acc, wave, lane, wm, wn);
+    DmaStep<C, 3, 2, 2 * PER>::run(Ab, Bb, m0, n0, kt + 3, true, as, bs, acc, wave, lane, wm, wn);
+  }
+  // Last four steps: only the first issues a load (tile KT - 1); the waits drain the pipeline.
+  DmaStep<C, 0, 3, 2 * PER>::run(Ab, Bb, m0, n0, kt, true, as, bs, acc, wave, lane, wm, wn);
+  DmaStep<C, 1, 0, 2 * PER>::run(Ab, Bb, m0, n0, kt + 1, false, as, bs, acc, wave, lane, wm, wn);
+  DmaStep<C, 2, 1, PER>::run(Ab, Bb, m0, n0, kt + 2, false, as, bs, acc, wave, lane, wm, wn);
+  DmaStep<C, 3, 2, 0>::run(Ab, Bb, m0, n0, kt + 3, false, as, bs, acc, wave, lane, wm, wn);
+
+  const long col_base = n0 + wn * (BN / 2) + (lane & 31);
+  const long row_base = m0 + wm * (BM / 2) + (lane >> 5) * 4;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) epi(batch, row_base + i * 32 + g * 8 + r, col_base + j * 32, acc[i][j][g * 4 + r]);
 }
 
 }  // namespace gemm

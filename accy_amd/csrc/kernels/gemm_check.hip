@@ -40,3 +40,27 @@ extern "C" __global__ void __launch_bounds__(256) accy_check_common(const float*
   v = accy::block_reduce<256>(v, accy::SumOp(), lds);
   if (threadIdx.x == 0) y[blockIdx.x] = accy::round_bf16(v);
 }
+
+struct CheckDmaNN {
+  static constexpr int DT = 0;
+  static constexpr long M = 8192, N = 8192, K = 8192;
+  static constexpr long A_B = 0, A_M = 8192, A_K = 1, B_B = 0, B_K = 8192, B_N = 1;
+  static constexpr bool A_KC = true, B_KC = false;
+  static constexpr int BM = 256, BN = 256;
+};
+
+struct CheckDmaTN {
+  static constexpr int DT = 1;
+  static constexpr long M = 384, N = 128, K = 256;
+  static constexpr long A_B = 0, A_M = 1, A_K = 384, B_B = 0, B_K = 1, B_N = 256;
+  static constexpr bool A_KC = false, B_KC = true;
+  static constexpr int BM = 128, BN = 128;
+};
+
+extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_nn(const u16_t* a, const u16_t* b, u16_t* c) {
+  accy::gemm::mma16_dma<CheckDmaNN>(a, b, CheckEpi{c, 8192});
+}
+
+extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_tn(const u16_t* a, const u16_t* b, u16_t* c) {
+  accy::gemm::mma16_dma<CheckDmaTN>(a, b, CheckEpi{c, 128});
+}

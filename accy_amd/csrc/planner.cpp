@@ -1,6 +1,8 @@
 // Kernel formation: walks the program in operation order and turns every value that must live in a
 // device buffer into a generated kernel. See lower.cpp for the fusion rules and the references.
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <set>
 #include <sstream>
 
@@ -706,7 +708,24 @@ class Planner {
     const Op& op = g_.ops[v];
     int out = slots_.slot_of[v] >= 0 ? slots_.slot_of[v] : temp_slot(v);
     DType d = op.result.dtype;
-    const int BM = 256, BN = 256, BK = 64, WM = 4, WN = 2;
+    // 256 x 256 x 64 tiles; the wave grid (4 x 2 waves of 64 x 128, or 2 x 2 waves of 128 x 128)
+    // can be overridden with ACCY_GEMM_WAVES=MxN for tuning.
+    const int BM = 256, BN = 256, BK = 64;
+    int WM = 2, WN = 2;
+    if (const char* s = std::getenv("ACCY_GEMM_WAVES")) {
+      int m = 0, n = 0;
+      if (std::sscanf(s, "%dx%d", &m, &n) == 2 && (m == 2 || m == 4) && (n == 2 || n == 4) && m * n <= 8) {
+        WM = m;
+        WN = n;
+      }
+    }
+    // Direct-to-LDS pipeline when the tiles divide the problem exactly (every row start 16-byte
+    // aligned); otherwise the register-staged kernel, which guards edges.
+    int dm = gs.m % 256 == 0 ? 256 : (gs.m % 128 == 0 ? 128 : 0);
+    int dn = gs.n % 256 == 0 ? 256 : (gs.n % 128 == 0 ? 128 : 0);
+    bool a_ok = (gs.a_k == 1 && gs.a_m % 8 == 0) || (gs.a_m == 1 && gs.a_k % 8 == 0);
+    bool b_ok = (gs.b_k == 1 && gs.b_n % 8 == 0) || (gs.b_n == 1 && gs.b_k % 8 == 0);
+    bool dma = dm && dn && gs.k % 128 == 0 && a_ok && b_ok && !std::getenv("ACCY_GEMM_NO_DMA");
     KernelWriter w(g_, slots_, "i64_t");
     std::string a = w.arg(gs.a.slot, false), b = w.arg(gs.b.slot, false), c = w.arg(out, true);
     std::string nm = name("gemm", v);
@@ -718,25 +737,30 @@ class Planner {
         << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", A_K = " << gs.a_k << ";\n"
         << "  static constexpr long B_B = " << gs.b_b << ", B_K = " << gs.b_k << ", B_N = " << gs.b_n << ";\n"
         << "  static constexpr bool A_KC = " << (gs.a_k == 1 ? "true" : "false")
-        << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n"
-        << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
-        << ", WAVES_N = " << WN << ";\n};\n";
+        << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n";
+    if (dma) {
+      src << "  static constexpr int BM = " << dm << ", BN = " << dn << ";\n};\n";
+    } else {
+      src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
+          << ", WAVES_N = " << WN << ";\n};\n";
+    }
     src << "struct Epi_" << nm << " {\n  u16_t* __restrict__ c;\n"
         << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
         << "    c[b * " << gs.m * gs.n << "L + m * " << gs.n << "L + n] = accy::f32_to_"
         << (d == DType::bf16 ? "bf16" : "f16") << "(v);\n  }\n};\n";
-    src << "extern \"C\" __global__ void __launch_bounds__(" << WM * WN * 64 << ") " << nm << "(const u16_t* __restrict__ "
+    int threads = dma ? 256 : WM * WN * 64;
+    src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(const u16_t* __restrict__ "
         << a << ", const u16_t* __restrict__ " << b << ", u16_t* __restrict__ " << c << ") {\n"
-        << "  accy::gemm::mma16<Cfg_" << nm << ">(" << a << " + " << gs.a.offset << "L, " << b << " + "
-        << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
+        << "  accy::gemm::" << (dma ? "mma16_dma" : "mma16") << "<Cfg_" << nm << ">(" << a << " + " << gs.a.offset
+        << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
     KernelStep k;
     k.source = src.str();
     k.name = nm;
-    int64_t tiles = ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
+    int64_t tiles = dma ? (gs.m / dm) * (gs.n / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
     k.grid[0] = (uint32_t)tiles;
     k.grid[1] = (uint32_t)gs.batch;
-    k.block[0] = WM * WN * 64;
-    k.shared_bytes = 2u * (BM + BN) * (BK + 8) * 2u;
+    k.block[0] = threads;
+    k.shared_bytes = dma ? 0u : 2u * (BM + BN) * (BK + 8) * 2u;
     k.klass = "gemm";
     k.label = "gemm:%" + std::to_string(v);
     k.algorithmic_flops = 2.0 * (double)gs.batch * (double)gs.m * (double)gs.n * (double)gs.k;

@@ -180,6 +180,29 @@ def test_gemm_mfma_transposed_lhs():
     assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16")
 
 
+@pytest.mark.parametrize("case", ["nn-256x512x384-bf16", "nn-128x256x128-f16", "tn-384x256x128-bf16",
+                                  "nt-batched-256x128x384-f16"])
+def test_gemm_direct_to_lds_layouts(case):
+    """Shapes the direct-to-LDS pipeline takes (exact tiles), in each operand layout."""
+    say(f"gemm dma {case}")
+    kind, shape, dtype = case.split("-")[0], case.split("-")[-2], case.split("-")[-1]
+    m, k, n = map(int, shape.split("x"))
+    if kind == "nn":
+        prog = W.gemm_program(m, k, n, dtype)
+        ins = W.gemm_inputs(m, k, n, dtype, seed=m + k)
+    elif kind == "tn":
+        prog = T.define("tn", [T.spec(dtype, k=k, m=m), T.spec(dtype, k=k, n=n)], lambda b, a: a[0].contract(a[1], "k"))
+        ins = [W.to_dtype(W.uniform(31, k * m, -1, 1), dtype).reshape(k, m),
+               W.to_dtype(W.uniform(32, k * n, -1, 1), dtype).reshape(k, n)]
+    else:
+        prog = _qk_program(2, m, n, k, dtype)
+        ins = [W.to_dtype(W.normal(33, 2 * m * k), dtype).reshape(2, m, k),
+               W.to_dtype(W.normal(34, 2 * n * k), dtype).reshape(2, n, k)]
+    src = hip.plan_source(prog)
+    assert "mma16_dma" in src, src[:400]
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype)
+
+
 def test_gemm_bf16_full_size_on_sampled_rows():
     say("gemm bf16 8192^3 (full)")
     a, b = W.gemm_inputs(8192, 8192, 8192, "bf16")

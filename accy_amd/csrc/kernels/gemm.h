@@ -255,30 +255,45 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Issues this wave's share of one operand tile. KC: rows of 32 k (64 bytes); else rows of k.
+// Waits for this wave's LDS reads, then meets the other waves. The empty asm statements keep the
+// optimiser from moving LDS accesses across the barrier (s_barrier alone is no memory fence, and a
+// real fence would also wait for every outstanding global load).
+__device__ __forceinline__ void lds_reads_done_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Issues load instruction i of this wave's share of one operand tile (ROWS * 64 bytes, 1 KiB per
+// wave instruction, INSTRS / 4 instructions per wave). KC: rows of 32 k (64 bytes); else rows of k.
+template <int ROWS, bool KC, long SR, long SK>
+__device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave,
+                                         int lane, int i) {
+  constexpr int INSTRS = ROWS * 64 / 1024;
+  static_assert(INSTRS % 4 == 0, "four waves share the tile");
+  const int gi = wave * (INSTRS / 4) + i;
+  const u16_t* src;
+  if constexpr (KC) {
+    const int q = (lane & 7) ^ (lane >> 3);  // logical slot of this lane's physical chunk
+    const int row = 16 * gi + 2 * (lane >> 3) + (q >> 2);
+    src = base + (r0 + row) * SR + k0 + 8 * (q & 3);
+  } else {
+    constexpr int ROWB = ROWS * 2;    // bytes per k row
+    constexpr int LPR = ROWB / 16;    // lanes per k row
+    constexpr int RPI = 1024 / ROWB;  // k rows per instruction
+    const int row = RPI * gi + lane / LPR;
+    const int p = lane % LPR;
+    const int u = (p >> 1) ^ (row & 7);
+    src = base + (k0 + row) * SK + r0 + 16 * u + 8 * (p & 1);
+  }
+  dma16(src, (ACCY_LDS void*)(lds + gi * 512));
+}
+
 template <int ROWS, bool KC, long SR, long SK>
 __device__ __forceinline__ void dma_tile(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int INSTRS = ROWS * 64 / 1024;  // 1 KiB per wave instruction
-  static_assert(INSTRS % 4 == 0, "four waves share the tile");
 #pragma unroll
-  for (int i = 0; i < INSTRS / 4; ++i) {
-    const int gi = wave * (INSTRS / 4) + i;
-    const u16_t* src;
-    if constexpr (KC) {
-      const int q = (lane & 7) ^ (lane >> 3);  // logical slot of this lane's physical chunk
-      const int row = 16 * gi + 2 * (lane >> 3) + (q >> 2);
-      src = base + (r0 + row) * SR + k0 + 8 * (q & 3);
-    } else {
-      constexpr int ROWB = ROWS * 2;                // bytes per k row
-      constexpr int LPR = ROWB / 16;                // lanes per k row
-      constexpr int RPI = 1024 / ROWB;              // k rows per instruction
-      const int row = RPI * gi + lane / LPR;
-      const int p = lane % LPR;
-      const int u = (p >> 1) ^ (row & 7);
-      src = base + (k0 + row) * SK + r0 + 16 * u + 8 * (p & 1);
-    }
-    dma16(src, (ACCY_LDS void*)(lds + gi * 512));
-  }
+  for (int i = 0; i < ROWS * 64 / 1024 / 4; ++i) dma_part<ROWS, KC, SR, SK>(base, r0, k0, lds, wave, lane, i);
 }
 
 // Fragment of 32 rows (M or N) x 16 k for one MFMA, read from a stage.
@@ -308,31 +323,74 @@ __device__ __forceinline__ u32x4 frag(const u16_t* lds, int row0, int s, int lan
   }
 }
 
-template <class C, int STAGE, int NEXT, int WAIT>
+// The fragments of one 16-deep sub-step for this wave's (BM / 2) x (BN / 2) sub-tile: TM A
+// fragments, then TN B fragments (fragment q of the set is loaded by load_one(q)).
+template <class C>
+struct Frags {
+  static constexpr int TM = C::BM / 64, TN = C::BN / 64, COUNT = TM + TN;
+  u32x4 a[TM], b[TN];
+  __device__ __forceinline__ void load_one(int q, const u16_t* as, const u16_t* bs, int s, int lane, int wm, int wn) {
+    if (q < TM)
+      a[q] = frag<C::BM, C::A_KC>(as, wm * (C::BM / 2) + q * 32, s, lane);
+    else
+      b[q - TM] = frag<C::BN, C::B_KC>(bs, wn * (C::BN / 2) + (q - TM) * 32, s, lane);
+  }
+  template <class Acc>
+  __device__ __forceinline__ void mma_one(int t, Acc& acc) const {
+    acc[t / TN][t % TN] = mfma32x32x16<C::DT>(a[t / TN], b[t % TN], acc[t / TN][t % TN]);
+  }
+};
+
+// One K step on stage STAGE. On entry f0 holds this step's first sub-step fragments and every wave
+// has finished reading the previous stage (NEXT). The first half runs the MFMAs of f0 with the
+// loads of tile kt + 3 into NEXT and the reads of this stage's second sub-step (f1) slotted between
+// them; then the wave waits for its own loads of tile kt + 1 and its LDS reads and meets the other
+// waves at the step's single barrier (after which tile kt + 1 is complete and nobody reads this
+// stage any more); the second half runs the MFMAs of f1 with the reads of tile kt + 1's first
+// sub-step (the next f0) between them. The explicit interleave keeps at most one sub-step of LDS
+// reads in flight, so the compiler's lgkmcnt waits stay exact instead of draining the counter.
+template <class C, int STAGE, int NEXT, int WAIT, bool ISSUE, bool HAS_NEXT>
 struct DmaStep {
   template <class Acc>
   __device__ __forceinline__ static void run(const u16_t* __restrict__ Ab, const u16_t* __restrict__ Bb, long m0,
-                                             long n0, long kt, bool issue, u16_t* const (&as)[4],
-                                             u16_t* const (&bs)[4], Acc& acc, int wave, int lane, int wm, int wn) {
-    constexpr int BM = C::BM, BN = C::BN;
-    constexpr int TM = BM / 64, TN = BN / 64;
-    wait_vmcnt<WAIT>();
-    __builtin_amdgcn_s_barrier();
-    if (issue) {
-      dma_tile<BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, (kt + 3) * 32, as[NEXT], wave, lane);
-      dma_tile<BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, (kt + 3) * 32, bs[NEXT], wave, lane);
+                                             long n0, long kt, u16_t* const (&as)[4], u16_t* const (&bs)[4],
+                                             Frags<C>& f0, Acc& acc, int wave, int lane, int wm, int wn) {
+    constexpr int NM = Frags<C>::TM * Frags<C>::TN, NF = Frags<C>::COUNT;
+    constexpr int DA = C::BM * 64 / 1024 / 4, DB = C::BN * 64 / 1024 / 4;
+    constexpr int ND = ISSUE ? DA + DB : 0, NI = NF + ND;
+    Frags<C> f1;
+#pragma unroll
+    for (int t = 0; t < NM; ++t) {
+      f0.mma_one(t, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      // Items: the f1 fragment reads first (they must land before the barrier), then the tile loads.
+#pragma unroll
+      for (int k = t * NI / NM; k < (t + 1) * NI / NM; ++k) {
+        if (k < NF) {
+          f1.load_one(k, as[STAGE], bs[STAGE], 1, lane, wm, wn);
+        } else if (k - NF < DA) {
+          dma_part<C::BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, (kt + 3) * 32, as[NEXT], wave, lane, k - NF);
+        } else {
+          dma_part<C::BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, (kt + 3) * 32, bs[NEXT], wave, lane, k - NF - DA);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (HAS_NEXT) {
+      wait_vmcnt<WAIT>();
+      lds_reads_done_barrier();
     }
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      u32x4 a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) a[i] = frag<BM, C::A_KC>(as[STAGE], wm * (BM / 2) + i * 32, s, lane);
-#pragma unroll
-      for (int j = 0; j < TN; ++j) b[j] = frag<BN, C::B_KC>(bs[STAGE], wn * (BN / 2) + j * 32, s, lane);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma32x32x16<C::DT>(a[i], b[j], acc[i][j]);
+    for (int t = 0; t < NM; ++t) {
+      f1.mma_one(t, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      // One next-f0 fragment read per MFMA from the start (NF <= NM), so the last one lands well
+      // before the next step's first MFMA.
+      if constexpr (HAS_NEXT) {
+        static_assert(NF <= NM, "fragment reads fit one per MFMA");
+        if (t < NF) f0.load_one(t, as[(STAGE + 1) & 3], bs[(STAGE + 1) & 3], 0, lane, wm, wn);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 };
@@ -369,18 +427,25 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
     dma_tile<BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, s * 32, as[s], wave, lane);
     dma_tile<BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, s * 32, bs[s], wave, lane);
   }
+  // Tile 0 complete everywhere (tiles 1 and 2 may still be in flight), then its first sub-step.
+  Frags<C> f0;
+  wait_vmcnt<2 * PER>();
+  lds_reads_done_barrier();
+#pragma unroll
+  for (int q = 0; q < Frags<C>::COUNT; ++q) f0.load_one(q, as[0], bs[0], 0, lane, wm, wn);
+  // Step kt issues tile kt + 3 and then waits for tile kt + 1: tiles kt + 2 and kt + 3 stay in flight.
   long kt = 0;
   for (; kt + 4 < KT; kt += 4) {
-    DmaStep<C, 0, 3, 2 * PER>::run(Ab, Bb, m0, n0, kt, true, as, bs, acc, wave, lane, wm, wn);
-    DmaStep<C, 1, 0, 2 * PER>::run(Ab, Bb, m0, n0, kt + 1, true, as, bs, acc, wave, lane, wm, wn);
-    DmaStep<C, 2, 1, 2 * PER>::run(Ab, Bb, m0, n0, kt + 2, true, as, bs, acc, wave, lane, wm, wn);
-    DmaStep<C, 3, 2, 2 * PER>::run(Ab, Bb, m0, n0, kt + 3, true, as, bs, acc, wave, lane, wm, wn);
+    DmaStep<C, 0, 3, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt, as, bs, f0, acc, wave, lane, wm, wn);
+    DmaStep<C, 1, 0, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt + 1, as, bs, f0, acc, wave, lane, wm, wn);
+    DmaStep<C, 2, 1, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt + 2, as, bs, f0, acc, wave, lane, wm, wn);
+    DmaStep<C, 3, 2, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt + 3, as, bs, f0, acc, wave, lane, wm, wn);
   }
   // Last four steps: only the first issues a load (tile KT - 1); the waits drain the pipeline.
-  DmaStep<C, 0, 3, 2 * PER>::run(Ab, Bb, m0, n0, kt, true, as, bs, acc, wave, lane, wm, wn);
-  DmaStep<C, 1, 0, 2 * PER>::run(Ab, Bb, m0, n0, kt + 1, false, as, bs, acc, wave, lane, wm, wn);
-  DmaStep<C, 2, 1, PER>::run(Ab, Bb, m0, n0, kt + 2, false, as, bs, acc, wave, lane, wm, wn);
-  DmaStep<C, 3, 2, 0>::run(Ab, Bb, m0, n0, kt + 3, false, as, bs, acc, wave, lane, wm, wn);
+  DmaStep<C, 0, 3, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt, as, bs, f0, acc, wave, lane, wm, wn);
+  DmaStep<C, 1, 0, PER, false, true>::run(Ab, Bb, m0, n0, kt + 1, as, bs, f0, acc, wave, lane, wm, wn);
+  DmaStep<C, 2, 1, 0, false, true>::run(Ab, Bb, m0, n0, kt + 2, as, bs, f0, acc, wave, lane, wm, wn);
+  DmaStep<C, 3, 2, 0, false, false>::run(Ab, Bb, m0, n0, kt + 3, as, bs, f0, acc, wave, lane, wm, wn);
 
   const long col_base = n0 + wn * (BN / 2) + (lane & 31);
   const long row_base = m0 + wm * (BM / 2) + (lane >> 5) * 4;

@@ -1,0 +1,36 @@
+// Build-time check (compiled by accy_amd/build.py with hipcc --offload-arch=gfx950): instantiates the
+// fused attention template for the shapes the planner emits, so that a host without a GPU still
+// verifies that it compiles for CDNA4. Nothing calls these kernels.
+#include "common.h"
+#include "gemm.h"
+#include "attention.h"
+
+struct CheckAttnF16 {
+  static constexpr int DT = 1, WAVES = 4;
+  static constexpr long SQ = 4096, SK = 4096, NB = 32;
+  static constexpr long Q_S = 128, K_S = 128, V_S = 128;
+  static constexpr bool CAUSAL = false;
+  static constexpr float SL = 0x1.fe0000p-4f;
+  static __device__ __forceinline__ long q_off(long b) { return b * 524288L; }
+  static __device__ __forceinline__ long k_off(long b) { return b * 524288L; }
+  static __device__ __forceinline__ long v_off(long b) { return b * 524288L; }
+};
+
+struct CheckAttnCausalBf16 {
+  static constexpr int DT = 0, WAVES = 4;
+  static constexpr long SQ = 2048, SK = 2048, NB = 64;
+  static constexpr long Q_S = 2048, K_S = 2048, V_S = 2048;
+  static constexpr bool CAUSAL = true;
+  static constexpr float SL = 0x1.fe0000p-4f;
+  static __device__ __forceinline__ long q_off(long b) { return (b / 16) * 4194304L + (b % 16) * 128L; }
+  static __device__ __forceinline__ long k_off(long b) { return (b / 16) * 4194304L + (b % 16) * 128L; }
+  static __device__ __forceinline__ long v_off(long b) { return (b / 16) * 4194304L + (b % 16) * 128L; }
+};
+
+extern "C" __global__ void __launch_bounds__(256) accy_check_attention_f16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
+  accy::attn::flash<CheckAttnF16>(q, k, v, o);
+}
+
+extern "C" __global__ void __launch_bounds__(256) accy_check_attention_causal_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
+  accy::attn::flash<CheckAttnCausalBf16>(q, k, v, o);
+}

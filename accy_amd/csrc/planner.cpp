@@ -1,8 +1,10 @@
 // Kernel formation: walks the program in operation order and turns every value that must live in a
 // device buffer into a generated kernel. See lower.cpp for the fusion rules and the references.
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <set>
 #include <sstream>
 
@@ -105,23 +107,11 @@ class Planner {
         needed_[v] = true;
       }
     }
+    match_attentions();
     mark_gemm_operands();
     for (uint32_t v = 0; v < n; ++v) {
       if (!live_[v] || done_[v]) continue;
-      const Op& op = g_.ops[v];
-      switch (op.kind) {
-        case Kind::parameter: break;
-        case Kind::reduce:
-          if (!row_group(v)) fold(v);
-          break;
-        case Kind::dot_general: dot(v); break;
-        case Kind::scatter_add: scatter_add(v); break;
-        case Kind::scan: case Kind::projection: case Kind::custom_call: case Kind::sparse_cross_entropy:
-          fail(Err::Unsupported, std::string(kind_name(op.kind)) + " is not supported by the HIP target");
-        default:
-          if (needed_[v]) map(v);
-          break;
-      }
+      process(v);
     }
     for (auto& c : copies) {
       uint32_t v = (uint32_t)c.first;
@@ -152,6 +142,23 @@ class Planner {
 
   // Index arithmetic is 32-bit unless some value of the program has 2^31 or more elements.
   std::string itype() const { return index_type(max_elems_); }
+
+  void process(uint32_t v) {
+    const Op& op = g_.ops[v];
+    switch (op.kind) {
+      case Kind::parameter: break;
+      case Kind::reduce:
+        if (!row_group(v)) fold(v);
+        break;
+      case Kind::dot_general: dot(v); break;
+      case Kind::scatter_add: scatter_add(v); break;
+      case Kind::scan: case Kind::projection: case Kind::custom_call: case Kind::sparse_cross_entropy:
+        fail(Err::Unsupported, std::string(kind_name(op.kind)) + " is not supported by the HIP target");
+      default:
+        if (needed_[v]) map(v);
+        break;
+    }
+  }
 
   void mark_live() {
     std::vector<uint32_t> stack(g_.outputs.begin(), g_.outputs.end());
@@ -669,7 +676,7 @@ class Planner {
   void mark_gemm_operands() {
     for (uint32_t v = 0; v < g_.ops.size(); ++v) {
       const Op& op = g_.ops[v];
-      if (!live_[v] || op.kind != Kind::dot_general) continue;
+      if (!live_[v] || op.kind != Kind::dot_general || attn_.count(v)) continue;
       if (op.result.dtype != DType::bf16 && op.result.dtype != DType::f16) continue;
       for (uint32_t a : op.args) {
         if (!view_chain_to_anchor(a)) needed_[a] = true;
@@ -694,8 +701,310 @@ class Planner {
     }
   }
 
+  // ---- fused attention: dot(softmax_last(scale * dot(Q, K) [causal -inf mask]), V) ----
+  //
+  // The pattern is the one attention programs trace (a contraction, a scale by a splat constant, an
+  // optional select of -inf where key > query, max, sub, exp, sum, div over the key axis, and the
+  // contraction with V). Its intermediate values are absorbed when nothing else uses them; the
+  // kernel computes the softmax in f32 online over key blocks (the accumulation order and the
+  // rounding of the intermediate scores and probabilities differ from per-op 16-bit evaluation).
+  struct Attn {
+    uint32_t qk = 0;
+    std::vector<uint32_t> inner;  // values computed only inside the fused kernel, in program order
+    double scale = 1.0;
+    bool causal = false;
+  };
+  std::map<uint32_t, Attn> attn_;
+
+  // Value of a splat float constant, seen through broadcasts.
+  bool splat_float(uint32_t v, double& out) const {
+    const Op* op = &g_.ops[v];
+    while (op->kind == Kind::broadcast_in_dim || op->kind == Kind::broadcast) op = &g_.ops[op->args[0]];
+    if (op->kind != Kind::constant || !is_splat_constant(*op) || op->bytes.size() < 2) return false;
+    const uint8_t* p = (const uint8_t*)op->bytes.data();
+    switch (op->result.dtype) {
+      case DType::f16: out = f16_bits_to_f32((uint16_t)(p[0] | (p[1] << 8))); return true;
+      case DType::bf16: out = bf16_bits_to_f32((uint16_t)(p[0] | (p[1] << 8))); return true;
+      case DType::f32: {
+        if (op->bytes.size() < 4) return false;
+        float f;
+        std::memcpy(&f, p, 4);
+        out = f;
+        return true;
+      }
+      default: return false;
+    }
+  }
+
+  // `v` = broadcast_in_dim(src) of a rank R-1 value back over the last axis of rank R.
+  bool row_broadcast_of(uint32_t v, size_t R, uint32_t& src) const {
+    const Op& op = g_.ops[v];
+    if (op.kind != Kind::broadcast_in_dim || op.ints.size() != R - 1 || op.result.rank() != R) return false;
+    for (size_t i = 0; i + 1 < R; ++i)
+      if (op.ints[i] != (int64_t)i) return false;
+    src = op.args[0];
+    return true;
+  }
+
+  bool reduces_last(const Op& op, size_t R) const {
+    return op.kind == Kind::reduce && op.ints.size() == 1 && op.ints[0] == (int64_t)R - 1 &&
+           g_.type(op.args[0]).rank() == R;
+  }
+
+  // Which axis of its own type the integer value `v` equals the coordinate of (iota seen through
+  // broadcast_in_dim), or -1.
+  int index_axis(uint32_t v) const {
+    const Op& op = g_.ops[v];
+    if (op.kind == Kind::iota) return (int)op.axis;
+    if (op.kind == Kind::broadcast_in_dim) {
+      int a = index_axis(op.args[0]);
+      return a < 0 ? -1 : (int)op.ints[(size_t)a];
+    }
+    return -1;
+  }
+
+  // `pred` (rank R) is true exactly where key index <= query index (query axis R-2, key axis R-1).
+  bool causal_mask(uint32_t pred, size_t R) const {
+    std::vector<int> map(R);
+    for (size_t i = 0; i < R; ++i) map[i] = (int)i;
+    uint32_t cur = pred;
+    while (g_.ops[cur].kind == Kind::broadcast_in_dim) {
+      const Op& b = g_.ops[cur];
+      std::vector<int> nm(b.ints.size());
+      for (size_t j = 0; j < b.ints.size(); ++j) nm[j] = map[(size_t)b.ints[j]];
+      map = nm;
+      cur = b.args[0];
+    }
+    const Op& c = g_.ops[cur];
+    if (c.kind != Kind::compare) return false;
+    int a = index_axis(c.args[0]), b = index_axis(c.args[1]);
+    if (a < 0 || b < 0) return false;
+    int sa = map[(size_t)a], sb = map[(size_t)b];
+    const int q = (int)R - 2, k = (int)R - 1;
+    Cmp cmp = (Cmp)c.code;
+    return (cmp == Cmp::ge && sa == q && sb == k) || (cmp == Cmp::le && sa == k && sb == q);
+  }
+
+  bool match_attention(uint32_t pv, Attn& at) const {
+    const Op& d = g_.ops[pv];
+    const DType dt = d.result.dtype;
+    if (d.kind != Kind::dot_general || (dt != DType::f16 && dt != DType::bf16)) return false;
+    const uint32_t pdiv = d.args[0];
+    const Op& dv = g_.ops[pdiv];
+    const size_t R = dv.result.rank();
+    if (R < 2 || dv.result.dtype != dt) return false;
+    if (d.lhs_contract.size() != 1 || d.lhs_contract[0] != (int64_t)R - 1 || d.lhs_batch.size() != R - 2) return false;
+    for (size_t i = 0; i + 2 < R; ++i)
+      if (d.lhs_batch[i] != (int64_t)i) return false;
+    if (dv.kind != Kind::binary || (Binary)dv.code != Binary::div) return false;
+    const uint32_t e = dv.args[0];
+    uint32_t sum, mx;
+    double init;
+    if (!row_broadcast_of(dv.args[1], R, sum)) return false;
+    const Op& so = g_.ops[sum];
+    if (!reduces_last(so, R) || (Reducer)so.code != Reducer::sum || so.args[0] != e) return false;
+    if (!splat_float(so.args[1], init) || init != 0.0) return false;
+    const Op& eo = g_.ops[e];
+    if (eo.kind != Kind::unary || (Unary)eo.code != Unary::exp) return false;
+    const uint32_t sub = eo.args[0];
+    const Op& subo = g_.ops[sub];
+    if (subo.kind != Kind::binary || (Binary)subo.code != Binary::sub) return false;
+    if (!row_broadcast_of(subo.args[1], R, mx)) return false;
+    const uint32_t s = subo.args[0];
+    const Op& mo = g_.ops[mx];
+    if (!reduces_last(mo, R) || (Reducer)mo.code != Reducer::max || mo.args[0] != s) return false;
+    if (!splat_float(mo.args[1], init) || !(std::isinf(init) && init < 0)) return false;
+    std::vector<uint32_t> inner = {pdiv, dv.args[1], sum, e, sub, subo.args[1], mx};
+    uint32_t x = s;
+    at.causal = false;
+    at.scale = 1.0;
+    if (g_.ops[x].kind == Kind::select) {
+      const Op& sel = g_.ops[x];
+      double f;
+      if (!splat_float(sel.args[2], f) || !(std::isinf(f) && f < 0) || !causal_mask(sel.args[0], R)) return false;
+      at.causal = true;
+      inner.push_back(x);
+      x = sel.args[1];
+    }
+    // Scale steps: multiplications or divisions by splat constants.
+    while (g_.ops[x].kind == Kind::binary) {
+      const Op& b = g_.ops[x];
+      inner.push_back(x);
+      double c;
+      if ((Binary)b.code == Binary::mul && splat_float(b.args[1], c)) {
+        at.scale *= c;
+        x = b.args[0];
+      } else if ((Binary)b.code == Binary::mul && splat_float(b.args[0], c)) {
+        at.scale *= c;
+        x = b.args[1];
+      } else if ((Binary)b.code == Binary::div && splat_float(b.args[1], c)) {
+        at.scale /= c;
+        x = b.args[0];
+      } else {
+        return false;
+      }
+    }
+    if (!(at.scale > 0) || !std::isfinite(at.scale)) return false;
+    const Op& qk = g_.ops[x];
+    if (qk.kind != Kind::dot_general || qk.result.dtype != dt || qk.result.dims != dv.result.dims) return false;
+    if (qk.lhs_contract.size() != 1 || qk.rhs_contract.size() != 1 || qk.lhs_batch.size() != R - 2) return false;
+    inner.push_back(x);
+    std::sort(inner.begin(), inner.end());
+    inner.erase(std::unique(inner.begin(), inner.end()), inner.end());
+    // Nothing outside the pattern may read an absorbed value.
+    for (uint32_t u = 0; u < g_.ops.size(); ++u) {
+      if (!live_[u] || u == pv || std::binary_search(inner.begin(), inner.end(), u)) continue;
+      for (uint32_t a : g_.ops[u].args)
+        if (std::binary_search(inner.begin(), inner.end(), a)) return false;
+    }
+    for (uint32_t o : g_.outputs)
+      if (std::binary_search(inner.begin(), inner.end(), o)) return false;
+    at.qk = x;
+    at.inner = inner;
+    return true;
+  }
+
+  void match_attentions() {
+    if (!opt_.allow_gemm) return;
+    for (uint32_t v = 0; v < g_.ops.size(); ++v) {
+      if (!live_[v] || g_.ops[v].kind != Kind::dot_general) continue;
+      Attn at;
+      if (!match_attention(v, at)) continue;
+      for (uint32_t u : at.inner) done_[u] = true;
+      attn_[v] = at;
+    }
+  }
+
+  struct AttnLayout {
+    int64_t sq = 0, sk = 0, nb = 1, q_s = 0, k_s = 0, v_s = 0;
+    std::vector<int64_t> extents, q_b, k_b, v_b;  // batch axes: extents and per-operand strides
+    View q, k, v;
+  };
+
+  static int free_axis(size_t rank, const std::vector<int64_t>& batch, const std::vector<int64_t>& contract) {
+    int f = -1;
+    for (size_t i = 0; i < rank; ++i) {
+      if (std::find(batch.begin(), batch.end(), (int64_t)i) != batch.end()) continue;
+      if (std::find(contract.begin(), contract.end(), (int64_t)i) != contract.end()) continue;
+      if (f >= 0) return -2;
+      f = (int)i;
+    }
+    return f;
+  }
+
+  bool attention_layout(uint32_t pv, const Attn& at, AttnLayout& L) const {
+    const Op& d = g_.ops[pv];
+    const Op& qk = g_.ops[at.qk];
+    if (!resolve_view(qk.args[0], L.q) || !resolve_view(qk.args[1], L.k) || !resolve_view(d.args[1], L.v)) return false;
+    const Type& qt = g_.type(qk.args[0]);
+    const Type& kt = g_.type(qk.args[1]);
+    const Type& vt = g_.type(d.args[1]);
+    const int qf = free_axis(qt.rank(), qk.lhs_batch, qk.lhs_contract);
+    const int kf = free_axis(kt.rank(), qk.rhs_batch, qk.rhs_contract);
+    const int vf = free_axis(vt.rank(), d.rhs_batch, d.rhs_contract);
+    if (qf < 0 || kf < 0 || vf < 0 || d.rhs_contract.size() != 1) return false;
+    const size_t qc = (size_t)qk.lhs_contract[0], kc = (size_t)qk.rhs_contract[0], vc = (size_t)d.rhs_contract[0];
+    if (qt.dims[qc].extent != 128 || kt.dims[kc].extent != 128 || vt.dims[(size_t)vf].extent != 128) return false;
+    if (L.q.strides[qc] != 1 || L.k.strides[kc] != 1 || L.v.strides[(size_t)vf] != 1) return false;
+    L.sq = qt.dims[(size_t)qf].extent;
+    L.sk = kt.dims[(size_t)kf].extent;
+    if (vt.dims[vc].extent != L.sk || L.sq % 64 != 0 || L.sk % 64 != 0 || L.sq == 0 || L.sk == 0) return false;
+    L.q_s = L.q.strides[(size_t)qf];
+    L.k_s = L.k.strides[(size_t)kf];
+    L.v_s = L.v.strides[vc];
+    auto ok8 = [](int64_t x) { return x % 8 == 0; };
+    if (!ok8(L.q_s) || !ok8(L.k_s) || !ok8(L.v_s) || !ok8(L.q.offset) || !ok8(L.k.offset) || !ok8(L.v.offset)) return false;
+    for (size_t i = 0; i < qk.lhs_batch.size(); ++i) {
+      const int64_t e = qt.dims[(size_t)qk.lhs_batch[i]].extent;
+      if (kt.dims[(size_t)qk.rhs_batch[i]].extent != e || vt.dims[(size_t)d.rhs_batch[i]].extent != e) return false;
+      L.extents.push_back(e);
+      L.q_b.push_back(L.q.strides[(size_t)qk.lhs_batch[i]]);
+      L.k_b.push_back(L.k.strides[(size_t)qk.rhs_batch[i]]);
+      L.v_b.push_back(L.v.strides[(size_t)d.rhs_batch[i]]);
+      if (!ok8(L.q_b.back()) || !ok8(L.k_b.back()) || !ok8(L.v_b.back())) return false;
+      L.nb *= e;
+    }
+    return L.nb > 0;
+  }
+
+  // Element offset of flattened (row-major) batch index b for one operand.
+  static std::string batch_offset(const std::vector<int64_t>& extents, const std::vector<int64_t>& strides,
+                                  int64_t offset) {
+    std::ostringstream s;
+    s << offset << "L";
+    int64_t inner = 1;
+    for (size_t i = extents.size(); i-- > 0;) {
+      if (extents[i] != 1 && strides[i] != 0) {
+        s << " + ((b / " << inner << "L) % " << extents[i] << "L) * " << strides[i] << "L";
+      }
+      inner *= extents[i];
+    }
+    return s.str();
+  }
+
+  void attention(uint32_t pv, const Attn& at, const AttnLayout& L) {
+    const Op& d = g_.ops[pv];
+    const DType dt = d.result.dtype;
+    int out = slots_.slot_of[pv] >= 0 ? slots_.slot_of[pv] : temp_slot(pv);
+    const int waves = L.sq % 256 == 0 ? 4 : (L.sq % 128 == 0 ? 2 : 1);
+    KernelWriter w(g_, slots_, "i64_t");
+    std::string q = w.arg(L.q.slot, false), k = w.arg(L.k.slot, false), v = w.arg(L.v.slot, false),
+                o = w.arg(out, true);
+    std::string nm = name("attention", pv);
+    char sl[64];
+    std::snprintf(sl, sizeof sl, "%af", (double)(float)(at.scale * 1.4426950408889634));
+    std::ostringstream src;
+    src << "#include \"gemm\"\n#include \"attention\"\n";
+    src << "struct Cfg_" << nm << " {\n"
+        << "  static constexpr int DT = " << (dt == DType::bf16 ? 0 : 1) << ", WAVES = " << waves << ";\n"
+        << "  static constexpr long SQ = " << L.sq << ", SK = " << L.sk << ", NB = " << L.nb << ";\n"
+        << "  static constexpr long Q_S = " << L.q_s << ", K_S = " << L.k_s << ", V_S = " << L.v_s << ";\n"
+        << "  static constexpr bool CAUSAL = " << (at.causal ? "true" : "false") << ";\n"
+        << "  static constexpr float SL = " << sl << ";\n"
+        << "  static __device__ __forceinline__ long q_off(long b) { return " << batch_offset(L.extents, L.q_b, L.q.offset)
+        << "; }\n"
+        << "  static __device__ __forceinline__ long k_off(long b) { return " << batch_offset(L.extents, L.k_b, L.k.offset)
+        << "; }\n"
+        << "  static __device__ __forceinline__ long v_off(long b) { return " << batch_offset(L.extents, L.v_b, L.v.offset)
+        << "; }\n};\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << nm << "(const u16_t* __restrict__ "
+        << q << ", const u16_t* __restrict__ " << k << ", const u16_t* __restrict__ " << v << ", u16_t* __restrict__ "
+        << o << ") {\n  accy::attn::flash<Cfg_" << nm << ">(" << q << ", " << k << ", " << v << ", " << o << ");\n}\n";
+    KernelStep ks;
+    ks.source = src.str();
+    ks.name = nm;
+    ks.grid[0] = (uint32_t)(L.nb * (L.sq / (64 * waves)));
+    ks.block[0] = 64 * waves;
+    ks.klass = "attention";
+    ks.label = "attention:%" + std::to_string(pv);
+    // Score pairs actually needed: all of them, or those with key <= query under the causal mask.
+    double pairs = (double)L.sq * (double)L.sk;
+    if (at.causal) {
+      const double n = (double)std::min(L.sq, L.sk);
+      pairs = n * (n + 1) / 2 + (L.sq > L.sk ? (double)(L.sq - L.sk) * (double)L.sk : 0.0);
+    }
+    ks.algorithmic_flops = 4.0 * (double)L.nb * pairs * 128.0;
+    push(std::move(ks), w);
+    finish(pv);
+  }
+
   void dot(uint32_t v) {
     const Op& op = g_.ops[v];
+    auto fused = attn_.find(v);
+    if (fused != attn_.end()) {
+      AttnLayout L;
+      if (attention_layout(v, fused->second, L)) {
+        attention(v, fused->second, L);
+        return;
+      }
+      // Operands the kernel cannot address: compute the absorbed values after all, in order.
+      needed_[op.args[0]] = true;
+      std::vector<uint32_t> inner = fused->second.inner;
+      attn_.erase(fused);
+      for (uint32_t u : inner) done_[u] = false;
+      for (uint32_t u : inner)
+        if (!done_[u]) process(u);
+    }
     GemmShape gs;
     if (gemm_eligible(op, gs)) {
       gemm(v, gs);

@@ -107,6 +107,49 @@ def assert_rel(got, ref, tol, dtype="f32"):
                            f"{(err / np.maximum(np.abs(r), 1e-300)).max():.3e} (tol {tol})")
 
 
+def exact_attention(q, k, v, scale, causal, dtype):
+    """softmax(scale * q k^T [key <= query]) v in float64 from the 16-bit inputs: the textbook
+    formula the reference's per-op evaluation approximates."""
+    q, k, v = (to_f32(np.asarray(x), dtype).astype(np.float64) for x in (q, k, v))
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) * scale
+    if causal:
+        keep = np.arange(s.shape[-1])[None, :] <= np.arange(s.shape[-2])[:, None]
+        s = np.where(keep, s, -np.inf)
+    e = np.exp(s - s.max(-1, keepdims=True))
+    return np.matmul(e / e.sum(-1, keepdims=True), v)
+
+
+def assert_attention(got, ref, tol, dtype, exact=None):
+    """Attention parity. Against runCpu's per-op 16-bit evaluation: max|g-r| / max|r| <= tol over the
+    whole output and over every query row. Against the float64 formula (when given): the error is
+    at most 1.5x runCpu's own plus a 16-bit rounding of the largest output. (A fused kernel keeps the
+    scores and probabilities in f32, so near-zero outputs differ from runCpu by runCpu's rounding
+    noise, and a per-element relative bound is not meaningful there.)"""
+    g = to_f32(np.asarray(got), dtype).astype(np.float64)
+    r = to_f32(np.asarray(ref), dtype).astype(np.float64)
+    assert g.shape == r.shape
+    if r.size == 0:
+        return
+    scale = np.abs(r).max()
+    err = np.abs(g - r)
+    assert err.max() <= tol * scale, f"normwise error {err.max() / scale:.3e} > {tol}"
+    row_scale = np.abs(r).max(-1)
+    row_err = err.max(-1)
+    bad = row_err > tol * np.maximum(row_scale, 1e-30)
+    ulp = 2.0 ** -10 if dtype == "f16" else 2.0 ** -7
+    if exact is not None:
+        # A row further than tol from runCpu passes only if it is closer to the exact result than
+        # runCpu's row is (few-key rows under a causal mask, where runCpu's own rounding dominates).
+        mine_rows = np.abs(g - exact).max(-1)
+        theirs_rows = np.abs(r - exact).max(-1)
+        bad &= mine_rows > 1.5 * theirs_rows + ulp * np.abs(exact).max(-1)
+    assert not bad.any(), f"{bad.sum()} of {bad.size} rows beyond {tol}: worst {(row_err / row_scale).max():.3e}"
+    if exact is not None:
+        mine = np.abs(g - exact).max()
+        theirs = np.abs(r - exact).max()
+        assert mine <= 1.5 * theirs + ulp * np.abs(exact).max(), f"error vs exact {mine:.3e}, runCpu's {theirs:.3e}"
+
+
 def assert_normwise(got, ref, tol, dtype="f32", floor=1e-3):
     """GEMM / attention parity: max|g-r| / max|r| <= tol, and per element
     |g-r| <= tol (|r| + floor max|r|)."""

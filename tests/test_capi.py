@@ -39,6 +39,8 @@ SMALL_PROGRAMS = {
     "gemm-bf16-mulsum": lambda: W.gemm_program(64, 64, 64, "bf16", "mulsum"),
     "attention": lambda: W.attention_program(2, 128, 64),
     "attention-causal": lambda: W.attention_program(2, 128, 64, causal=True),
+    "attention-fused": lambda: W.attention_program(2, 256, 128, "f16"),
+    "attention-fused-causal-bf16": lambda: W.attention_program(1, 128, 128, "bf16", causal=True),
     "decoder": lambda: W.decoder_program(1, 64, 128, 2, 64, 256),
 }
 
@@ -47,6 +49,34 @@ SMALL_PROGRAMS = {
 def test_every_config_program_lowers_and_compiles_for_gfx950(name):
     src = hip.plan_source(SMALL_PROGRAMS[name](), compile=True)
     assert "__global__" in src
+
+
+@pytest.mark.parametrize("prog,fused", [
+    (lambda: W.attention_program(32, 4096, 128, "f16"), True),
+    (lambda: W.attention_program(2, 384, 128, "bf16", causal=True), True),
+    (lambda: W.decoder_program(), True),
+    (lambda: W.attention_program(2, 128, 64), False),     # head dimension 64: unfused kernels
+    (lambda: W.attention_program(2, 96, 128), False),     # 96 queries: not a multiple of 64
+])
+def test_attention_fusion_decision(prog, fused):
+    src = hip.plan_source(prog(), compile=False)
+    assert ("accy::attn::flash" in src) == fused
+    if fused:
+        # scores, softmax and the product with V in one kernel: no 16-bit score buffer is planned
+        assert src.count("accy::attn::flash<") == 1
+
+
+def test_attention_fusion_keeps_values_read_elsewhere():
+    # the probabilities are also an output, so they must be materialised: no fusion
+    def body(b, a):
+        q, k, v = a
+        s = q.contract(k.rename("query", "key"), "dim").mul(b.full_float(T.Type("f16", ()), 0.125))
+        e = s.sub(s.max("key")).exp()
+        p = e.div(e.sum("key"))
+        return [p.contract(v.rename("query", "key"), "key"), p]
+    specs = [T.spec("f16", head=1, query=128, dim=128)] * 3
+    src = hip.plan_source(T.define("twice", specs, body), compile=False)
+    assert "accy::attn::flash" not in src
 
 
 def test_indexing_and_integer_programs_compile():

@@ -1,8 +1,10 @@
 """Parity of the gfx950 target with the CPU oracle, through the C ABI, on an MI355X.
 
-Tolerances (BASELINE parity table): f32 reductions relative 1e-5 per element; f32 GEMM / attention
-1e-3 normwise plus per element with a floor; bf16 / f16 2e-2 in the same two forms; integer, index
-and i1 results, and 16-bit add/sub/mul/div chains, bit-exact.
+Tolerances (BASELINE parity table): f32 reductions relative 1e-5 per element; f32 GEMM 1e-3
+normwise plus per element with a floor; bf16 / f16 2e-2 in the same two forms; the fused attention
+kernel 2e-2 normwise over the output and over every query row, and no less accurate than runCpu
+against the float64 formula; integer, index and i1 results, and 16-bit add/sub/mul/div chains,
+bit-exact.
 """
 import math
 
@@ -12,7 +14,8 @@ import pytest
 from accy_amd import hip
 from accy_amd import tensor as T
 from accy_amd import workloads as W
-from conftest import assert_normwise, assert_rel, hip_run, oracle_run, out_arrays
+from conftest import (assert_attention, assert_normwise, assert_rel, exact_attention, hip_run, oracle_run,
+                      out_arrays, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -142,6 +145,64 @@ def test_small_attention_and_decoder():
     prog = W.decoder_program(1, 16, 64, 2, 32, 128, dtype="bf16")
     ins = W.decoder_inputs(1, 16, 64, 2, 32, 128, dtype="bf16", seed=7)
     assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16")
+
+
+# ---- fused attention: one kernel for scores, online softmax and P.V ----
+
+def _fused(prog):
+    return "accy::attn::flash" in hip.plan_source(prog.encode(), compile=False)
+
+
+def _scale(dtype):
+    """The program's 1/sqrt(128) constant as the 16-bit value it is traced with."""
+    return float(to_f32(W.to_dtype(np.array([1 / math.sqrt(128)]), dtype), dtype)[0])
+
+
+@pytest.mark.parametrize("heads,seq,dtype,causal", [
+    (2, 256, "f16", False), (2, 256, "f16", True), (3, 384, "bf16", True), (1, 128, "bf16", False),
+    (2, 64, "f16", False), (1, 64, "f16", True)])
+def test_fused_attention_matches_oracle(heads, seq, dtype, causal):
+    say(f"attention {heads} x {seq} x 128 {dtype} causal={causal}")
+    prog = W.attention_program(heads, seq, 128, dtype, causal)
+    assert _fused(prog)
+    ins = W.attention_inputs(heads, seq, 128, dtype, seed=seq + heads)
+    exact = exact_attention(*ins, _scale(dtype), causal, dtype)
+    assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype, exact)
+
+
+def test_fused_attention_more_keys_than_queries():
+    say("attention 2 x 128 queries x 512 keys f16")
+    specs = [T.spec("f16", head=2, query=128, dim=128), T.spec("f16", head=2, key=512, dim=128),
+             T.spec("f16", head=2, key=512, dim=128)]
+    prog = T.define("cross", specs, W.attention_body("f16", 128))
+    assert _fused(prog)
+    shapes = [(2, 128, 128), (2, 512, 128), (2, 512, 128)]
+    ins = [W.to_dtype(W.normal(40 + i, int(np.prod(s))), "f16").reshape(s) for i, s in enumerate(shapes)]
+    exact = exact_attention(*ins, _scale("f16"), False, "f16")
+    assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "f16", exact)
+
+
+def test_attention_full_size_on_sampled_heads():
+    say("attention f16 32 x 4096 x 4096 x 128 (full)")
+    q, k, v = W.attention_inputs(32, 4096, 128, "f16")
+    prog = W.attention_program(32, 4096, 128, "f16")
+    assert _fused(prog)
+    got = hip_run(prog, [q, k, v])[0]
+    heads = [0, 31]
+    sub = [q[heads], k[heads], v[heads]]
+    ref = oracle_run(W.attention_program(2, 4096, 128, "f16"), sub)[0]
+    assert_attention(got[heads], ref, 2e-2, "f16", exact_attention(*sub, _scale("f16"), False, "f16"))
+
+
+def test_decoder_with_fused_causal_attention():
+    say("decoder 1 x 128 x 256, 2 heads x 128, ffn 512, bf16")
+    prog = W.decoder_program(1, 128, 256, 2, 128, 512, dtype="bf16")
+    assert _fused(prog)
+    ins = W.decoder_inputs(1, 128, 256, 2, 128, 512, dtype="bf16", seed=8)
+    # The residual stream (|x| ~ max|out|) is rounded to bf16 after every op, so the attention's
+    # f32 softmax moving one intermediate by one ulp (2^-8 of max|out|) is an absolute error floor
+    # where x1 + mlp cancels: per element the slack is 2e-2 * 0.05 max|out| = 2^-8 max|out| / 4.
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16", floor=0.05)
 
 
 # ---- contractions on the MFMA template ----

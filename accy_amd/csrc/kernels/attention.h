@@ -40,13 +40,25 @@ using gemm::i16x4;
 using gemm::u32x4;
 typedef u32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int HD = 128;  // head dimension of Q, K and V
-constexpr int BK = 64;   // keys per block
+// Compile-time loop: For<B, E>::run(f) calls f(Int<i>{}) for i = B .. E - 1, so that every register
+// array index in the body is a constant.
+template <int N> struct Int { static constexpr int value = N; };
+template <int B, int E> struct For {
+  template <class F> __device__ __forceinline__ static void run(F&& f) {
+    if constexpr (B < E) {
+      f(Int<B>{});
+      For<B + 1, E>::run(f);
+    }
+  }
+};
 
-// Issues this wave's share of the K tile of keys [k0, k0 + 64): 16 instructions of 4 rows each.
+constexpr int HD = 128;  // head dimension of Q, K and V
+constexpr int BK = 32;   // keys per block
+
+// Issues this wave's share of the K tile of keys [k0, k0 + 32): 8 instructions of 4 rows each.
 template <int WAVES, long KS>
 __device__ __forceinline__ void load_k(const u16_t* __restrict__ kb, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int PER = 16 / WAVES;
+  constexpr int PER = 8 / WAVES;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int gi = wave * PER + i;
@@ -58,7 +70,7 @@ __device__ __forceinline__ void load_k(const u16_t* __restrict__ kb, long k0, u1
 
 template <int WAVES, long VS>
 __device__ __forceinline__ void load_v(const u16_t* __restrict__ vb, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int PER = 16 / WAVES;
+  constexpr int PER = 8 / WAVES;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int gi = wave * PER + i;
@@ -69,9 +81,9 @@ __device__ __forceinline__ void load_v(const u16_t* __restrict__ vb, long k0, u1
   }
 }
 
-// A operand of S^T for key tile kt (32 keys) and head-dim step dd (16 elements).
-__device__ __forceinline__ u32x4 k_frag(const u16_t* lds, int kt, int dd, int lane) {
-  const int row = kt * 32 + (lane & 31);
+// A operand of S^T for the block's 32 keys and head-dim step dd (16 elements).
+__device__ __forceinline__ u32x4 k_frag(const u16_t* lds, int dd, int lane) {
+  const int row = lane & 31;
   const int c = 2 * dd + (lane >> 5);
   return *(const u32x4*)(lds + row * HD + ((c ^ (row & 15)) << 3));
 }
@@ -94,14 +106,72 @@ __device__ __forceinline__ u32x4 v_frag(const u16_t* lds, int dt, int s, int lan
 
 template <int DT>
 __device__ __forceinline__ u32_t pack2(float a, float b) {
-  if constexpr (DT == 0) return (u32_t)f32_to_bf16(a) | ((u32_t)f32_to_bf16(b) << 16);
-  else return (u32_t)f32_to_f16(a) | ((u32_t)f32_to_f16(b) << 16);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  if constexpr (DT == 0) {
+    typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(u32_t, __builtin_convertvector(f32x2{a, b}, b16x2));  // v_cvt_pk_bf16_f32 (RNE)
+  } else {
+    typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(u32_t, __builtin_convertvector(f32x2{a, b}, h16x2));  // v_cvt_pk_f16_f32 (RNE)
+  }
 }
 
+// max(a, b, c) in one v_max3_f32. (fmaxf on MFMA results costs a canonicalising v_max per value
+// on top of the comparison; the scores here are never signalling NaNs.)
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// acc + p.lo + p.hi for a packed pair of 16-bit probabilities, in one v_dot2_f32_{f16,bf16}: the row
+// sum accumulates in f32 exactly the rounded values that the P.V product uses.
+template <int DT>
+__device__ __forceinline__ float add_pair(u32_t p, float acc) {
+  if constexpr (DT == 0) {
+    typedef __bf16 b16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(b16x2, p), b16x2{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+  } else {
+    typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h16x2, p), h16x2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+  }
+}
+
+// x[l] and x[l ^ 32] for every lane l. v_permlane32_swap exchanges the upper 32 lanes of its first
+// operand with the lower 32 lanes of its second, so swapping x with a copy of itself leaves lane l
+// holding x[l] in one register and x[l ^ 32] in the other. It is written as inline assembly with
+// two distinct read-write registers (the compiler's builtin for it, used on two copies of one
+// value, kept only one of the results here), with wait states around it for the VALU writes and
+// reads of its operands.
+__device__ __forceinline__ void with_partner(float x, float& r0, float& r1) {
+  u32_t a = __builtin_bit_cast(u32_t, x), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  r0 = __builtin_bit_cast(float, a);
+  r1 = __builtin_bit_cast(float, b);
+}
+__device__ __forceinline__ float max_with_partner(float x) {
+  float a, b;
+  with_partner(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_with_partner(float x) {
+  float a, b;
+  with_partner(x, a, b);
+  return a + b;
+}
+
+// Software pipeline per wave, iteration j (key block j of 32 keys):
+//   A: the 16 MFMAs of S(j) = K(j) Q^T, with the softmax of block j - 1 slotted between them
+//      (slots 0-3 row maxima, slot 4 the exchange with the partner lane and the rare rescale,
+//      slots 5-15 exp2, partial sums and packing of P(j - 1));
+//   B: the 16 MFMAs of O^T += V(j - 1)^T P(j - 1)^T.
+// The softmax VALU work of one block thus issues under the MFMAs of the next. S alternates between
+// two register sets by block parity (no copies); K and V stages are four deep, because V(j - 1) is
+// still read while block j + 2 is loading.
 template <class C>
 struct Flash {
-  static constexpr int WAVES = C::WAVES, BQ = 64 * WAVES, QT = 2, KT = BK / 32, DS = HD / 16, DTN = HD / 32;
-  static constexpr int PER = 2 * (16 / WAVES);  // load instructions per wave per key block
+  static constexpr int WAVES = C::WAVES, BQ = 64 * WAVES, QT = 2, DS = HD / 16, DTN = HD / 32;
+  static constexpr int PER = 2 * (8 / WAVES);  // load instructions per wave per key block
   static constexpr long NQB = C::SQ / BQ, NKB = C::SK / BK;
   static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
 
@@ -111,6 +181,7 @@ struct Flash {
   u16_t* const* vs;
   u32x4 qf[QT][DS];
   f32x16 o[QT][DTN];
+  f32x16 s[2][QT];  // scores of the blocks of even / odd index
   float m[QT], l[QT];
   long q0;
   int wave, lane;
@@ -123,92 +194,137 @@ struct Flash {
     load_v<WAVES, C::V_S>(vb, j * BK, vs[ST], wave, lane);
   }
 
-  // Key block j from stage ST; block j + 2 goes to stage NX once every wave is past block j - 1.
-  template <int ST, int NX>
-  __device__ __forceinline__ void step(long j, long nkb) {
+  // Scores of keys above the query are -inf (blocks that cross the diagonal only).
+  template <int PB>
+  __device__ __forceinline__ void mask(long k0) {
+    if (k0 + BK - 1 <= q0) return;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const long qi = query(qt);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const long ki = k0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (ki > qi) s[PB][qt][r] = -__builtin_inff();
+      }
+    }
+  }
+
+  // Softmax work of slot T (see above) on the scores in set PB; p receives P as MFMA B operands.
+  template <int PB, int T>
+  __device__ __forceinline__ void softmax_slot(float (&mx)[QT], float (&msub)[QT], float (&ls)[QT][4], u32x4 (&p)[QT][2]) {
+    f32x16 (&sp)[QT] = s[PB];
+    if constexpr (T < 4) {
+      constexpr int qt = T >> 1, r0 = 8 * (T & 1);
+#pragma unroll
+      for (int r = 0; r < 8; r += 2) mx[qt] = max3(mx[qt], sp[qt][r0 + r], sp[qt][r0 + r + 1]);
+    } else if constexpr (T == 4) {
+      bool need[QT];
+      float mn[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        mn[qt] = max_with_partner(mx[qt]) * C::SL;
+        need[qt] = mn[qt] > m[qt] + 8.0f;
+      }
+      if (__any(need[0] || need[1])) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          const float alpha = need[qt] ? __builtin_amdgcn_exp2f(m[qt] - mn[qt]) : 1.0f;
+          m[qt] = need[qt] ? mn[qt] : m[qt];
+          l[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DTN; ++dt) o[qt][dt] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) msub[qt] = m[qt] == -__builtin_inff() ? 0.0f : m[qt];
+    } else {
+      // 32 elements over slots 5..15; element e: qt = e / 16, r = e % 16.
+      For<(T - 5) * 32 / 11, (T - 4) * 32 / 11>::run([&](auto ei) {
+        constexpr int e = decltype(ei)::value, qt = e >> 4, r = e & 15;
+        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][r], C::SL, -msub[qt]));
+        sp[qt][r] = x;
+        if constexpr (r & 1) {
+          const u32_t pair = pack2<C::DT>(sp[qt][r - 1], x);
+          p[qt][r >> 3][(r & 7) >> 1] = pair;
+          ls[qt][(r >> 1) & 3] = add_pair<C::DT>(pair, ls[qt][(r >> 1) & 3]);
+        }
+      });
+    }
+  }
+
+  // Phase A of block j (scores into set SB from stage ST) with the softmax of set PB when PREV.
+  template <int ST, int SB, int PB, bool PREV>
+  __device__ __forceinline__ void scores(long kprev0, u32x4 (&p)[QT][2]) {
+    const u16_t* kl = ks[ST];
+    float mx[QT], msub[QT], ls[QT][4];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      mx[qt] = -__builtin_inff();
+      msub[qt] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ls[qt][i] = 0.0f;
+      s[SB][qt] = f32x16{};
+    }
+    if constexpr (PREV && C::CAUSAL) mask<PB>(kprev0);
+    u32x4 a = k_frag(kl, 0, lane), an = a;
+    For<0, 16>::run([&](auto ti) {
+      constexpr int t = decltype(ti)::value, dd = t >> 1, qt = t & 1;
+      if constexpr (qt == 0 && t + 2 < 16) an = k_frag(kl, (t + 2) >> 1, lane);
+      s[SB][qt] = gemm::mfma32x32x16<C::DT>(a, qf[qt][dd], s[SB][qt]);
+      if constexpr (qt == 1) a = an;
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (PREV) softmax_slot<PB, t>(mx, msub, ls, p);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    if constexpr (PREV) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) l[qt] += (ls[qt][0] + ls[qt][1]) + (ls[qt][2] + ls[qt][3]);
+    }
+  }
+
+  // Phase B: O^T += V^T P^T for the block whose V tile is in stage VST.
+  template <int VST>
+  __device__ __forceinline__ void pv(const u32x4 (&p)[QT][2]) {
+    const u16_t* vl = vs[VST];
+    u32x4 a = v_frag(vl, 0, 0, lane), an = a;
+    For<0, 16>::run([&](auto ti) {
+      constexpr int t = decltype(ti)::value, dt = t >> 2, st = (t >> 1) & 1, qt = t & 1;
+      if constexpr (qt == 0 && t + 2 < 16) an = v_frag(vl, (t + 2) >> 2, ((t + 2) >> 1) & 1, lane);
+      o[qt][dt] = gemm::mfma32x32x16<C::DT>(a, p[qt][st], o[qt][dt]);
+      if constexpr (qt == 1) a = an;
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+
+  // Iteration j >= 1 on stage ST = j % 4.
+  template <int ST>
+  __device__ __forceinline__ void iteration(long j, long nkb) {
     if (j + 1 < nkb) gemm::wait_vmcnt<PER>();
     else gemm::wait_vmcnt<0>();
     gemm::lds_reads_done_barrier();
-    if (j + 2 < nkb) issue<NX>(j + 2);
-    const u16_t* kl = ks[ST];
-    const u16_t* vl = vs[ST];
-    const long k0 = j * BK;
+    if (j + 2 < nkb) issue<(ST + 2) & 3>(j + 2);
+    u32x4 p[QT][2];
+    scores<ST, ST & 1, (ST + 1) & 1, true>((j - 1) * BK, p);
+    pv<(ST + 3) & 3>(p);
+  }
 
-    f32x16 s[QT][KT];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt) s[qt][kt] = f32x16{};
-#pragma unroll
-    for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-      for (int dd = 0; dd < DS; ++dd) {
-        const u32x4 a = k_frag(kl, kt, dd, lane);
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) s[qt][kt] = gemm::mfma32x32x16<C::DT>(a, qf[qt][dd], s[qt][kt]);
-      }
-
-    if constexpr (C::CAUSAL) {
-      if (k0 + BK - 1 > q0) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          const long qi = query(qt);
-#pragma unroll
-          for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const long ki = k0 + 32 * kt + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-              if (ki > qi) s[qt][kt][r] = -__builtin_inff();
-            }
-        }
-      }
-    }
-
-    u32x4 p[QT][BK / 16];
+  // Softmax and P.V of the last block, in set PB and stage VST (no scores to overlap with).
+  template <int PB, int VST>
+  __device__ __forceinline__ void last(long k0) {
+    if constexpr (C::CAUSAL) mask<PB>(k0);
+    float mx[QT], msub[QT], ls[QT][4];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-      float mx = s[qt][0][0];
+      mx[qt] = -__builtin_inff();
+      msub[qt] = 0.0f;
 #pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[qt][kt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = mx * C::SL;
-      const bool need = mn > m[qt] + 8.0f;
-      if (__any(need)) {
-        const float alpha = need ? __builtin_amdgcn_exp2f(m[qt] - mn) : 1.0f;
-        m[qt] = need ? mn : m[qt];
-        l[qt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DTN; ++dt) o[qt][dt] *= alpha;
-      }
-      const float msub = m[qt] == -__builtin_inff() ? 0.0f : m[qt];
-      float sum = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < KT; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qt][kt][r], C::SL, -msub));
-          s[qt][kt][r] = e;
-          sum += e;
-        }
-      l[qt] += sum;
-#pragma unroll
-      for (int st = 0; st < BK / 16; ++st) {
-        const int kt = st >> 1, b = 8 * (st & 1);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) p[qt][st][w] = pack2<C::DT>(s[qt][kt][b + 2 * w], s[qt][kt][b + 2 * w + 1]);
-      }
+      for (int i = 0; i < 4; ++i) ls[qt][i] = 0.0f;
     }
-
+    u32x4 p[QT][2];
+    For<0, 16>::run([&](auto ti) { softmax_slot<PB, decltype(ti)::value>(mx, msub, ls, p); });
 #pragma unroll
-    for (int dt = 0; dt < DTN; ++dt)
-#pragma unroll
-      for (int st = 0; st < BK / 16; ++st) {
-        const u32x4 a = v_frag(vl, dt, st, lane);
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) o[qt][dt] = gemm::mfma32x32x16<C::DT>(a, p[qt][st], o[qt][dt]);
-      }
+    for (int qt = 0; qt < QT; ++qt) l[qt] += (ls[qt][0] + ls[qt][1]) + (ls[qt][2] + ls[qt][3]);
+    pv<VST>(p);
   }
 };
 
@@ -216,10 +332,10 @@ template <class C>
 __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
                                       const u16_t* __restrict__ V, u16_t* __restrict__ O) {
   using F = Flash<C>;
-  __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD];
-  __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD];
-  u16_t* const ks[3] = {k0s, k1s, k2s};
-  u16_t* const vs[3] = {v0s, v1s, v2s};
+  __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
+  __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
+  u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
+  u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
 
   // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
   // query blocks with the most keys start first.
@@ -259,25 +375,46 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   }
   f.template issue<0>(0);
   if (nkb > 1) f.template issue<1>(1);
-  for (long j = 0; j < nkb; j += 3) {
-    f.template step<0, 2>(j, nkb);
-    if (j + 1 < nkb) f.template step<1, 0>(j + 1, nkb);
-    if (j + 2 < nkb) f.template step<2, 1>(j + 2, nkb);
+  // Block 0: scores only.
+  {
+    if (nkb > 1) gemm::wait_vmcnt<F::PER>();
+    else gemm::wait_vmcnt<0>();
+    gemm::lds_reads_done_barrier();
+    if (nkb > 2) f.template issue<2>(2);
+    u32x4 unused[F::QT][2];
+    f.template scores<0, 0, 1, false>(0, unused);
+  }
+  long j = 1;
+  for (; j + 3 < nkb; j += 4) {
+    f.template iteration<1>(j, nkb);
+    f.template iteration<2>(j + 1, nkb);
+    f.template iteration<3>(j + 2, nkb);
+    f.template iteration<0>(j + 3, nkb);
+  }
+  if (j < nkb) f.template iteration<1>(j, nkb);
+  if (j + 1 < nkb) f.template iteration<2>(j + 1, nkb);
+  if (j + 2 < nkb) f.template iteration<3>(j + 2, nkb);
+  // The last block (index nkb - 1) still needs its softmax and P.V.
+  const long lb = nkb - 1;
+  switch (lb & 3) {
+    case 0: f.template last<0, 0>(lb * BK); break;
+    case 1: f.template last<1, 1>(lb * BK); break;
+    case 2: f.template last<0, 2>(lb * BK); break;
+    default: f.template last<1, 3>(lb * BK); break;
   }
 
   const int h = f.lane >> 5;
 #pragma unroll
   for (int qt = 0; qt < F::QT; ++qt) {
-    const float lt = f.l[qt] + __shfl_xor(f.l[qt], 32);
-    const float inv = 1.0f / lt;
+    const float inv = 1.0f / sum_with_partner(f.l[qt]);
     u16_t* __restrict__ orow = O + (b * C::SQ + f.query(qt)) * HD;
 #pragma unroll
     for (int dt = 0; dt < F::DTN; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const f32x16& acc = f.o[qt][dt];
-        u32_t lo = pack2<C::DT>(acc[4 * g] * inv, acc[4 * g + 1] * inv);
-        u32_t hi = pack2<C::DT>(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
+        const u32_t lo = pack2<C::DT>(acc[4 * g] * inv, acc[4 * g + 1] * inv);
+        const u32_t hi = pack2<C::DT>(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
         *(u32x2*)(orow + dt * 32 + 8 * g + 4 * h) = u32x2{lo, hi};
       }
   }

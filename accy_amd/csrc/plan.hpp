@@ -23,6 +23,9 @@ struct SlotInfo {
   std::string data;  // Const payload, uploaded once at compile time
 };
 
+// A generated source containing this line is compiled with MFMA results in VGPRs.
+constexpr const char* kMfmaVgprForm = "// accy: mfma-vgpr-form\n";
+
 struct KernelStep {
   std::string source;        // complete HIP source, compiled with hiprtc
   std::string name;          // extern "C" symbol in `source`

@@ -954,7 +954,7 @@ class Planner {
     char sl[64];
     std::snprintf(sl, sizeof sl, "%af", (double)(float)(at.scale * 1.4426950408889634));
     std::ostringstream src;
-    src << "#include \"gemm\"\n#include \"attention\"\n";
+    src << kMfmaVgprForm << "#include \"gemm\"\n#include \"attention\"\n";
     src << "struct Cfg_" << nm << " {\n"
         << "  static constexpr int DT = " << (dt == DType::bf16 ? 0 : 1) << ", WAVES = " << waves << ";\n"
         << "  static constexpr long SQ = " << L.sq << ", SK = " << L.sk << ", NB = " << L.nb << ";\n"

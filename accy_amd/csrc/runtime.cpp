@@ -70,10 +70,16 @@ std::vector<char> compile_kernel_source(const std::string& source, const std::st
   hiprtcProgram prog;
   if (hiprtcCreateProgram(&prog, source.c_str(), (name + ".hip").c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS)
     throw HipFailure(kStatusCompileFailed, "hiprtcCreateProgram failed");
-  // Packed-f32 instructions stay disabled for every kernel this target builds.
-  const char* opts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
-                        "-Xclang", "-packed-fp32-ops"};
-  hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts);
+  // Packed-f32 instructions stay disabled for every kernel this target builds. A source that
+  // contains the line kMfmaVgprForm asks for MFMA results in VGPRs (the fused attention kernel,
+  // whose VALU softmax reads every score: with accumulators in AGPRs each read is an extra copy).
+  std::vector<const char*> opts = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+                                   "-Xclang", "-packed-fp32-ops"};
+  if (source.find(kMfmaVgprForm) != std::string::npos) {
+    opts.push_back("-mllvm");
+    opts.push_back("-amdgpu-mfma-vgpr-form");
+  }
+  hiprtcResult r = hiprtcCompileProgram(prog, (int)opts.size(), opts.data());
   if (r != HIPRTC_SUCCESS) {
     size_t n = 0;
     hiprtcGetProgramLogSize(prog, &n);

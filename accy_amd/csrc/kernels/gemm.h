@@ -459,5 +459,119 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
         for (int r = 0; r < 4; ++r) epi(batch, row_base + i * 32 + g * 8 + r, col_base + j * 32, acc[i][j][g * 4 + r]);
 }
 
+
+// ---------------------------------------------------------------------------------------------
+// f32 contraction on v_mfma_f32_32x32x2_f32 (exact f32 products, f32 accumulation).
+//
+// 256 x 256 block tile, 4 wavefronts of 128 x 128 (4 x 4 accumulators of 32 x 32), K steps of 32
+// staged straight from global memory into LDS (global_load_lds_dwordx4), two stages: one K step
+// is 256 MFMAs per wave, long enough to cover the next step's loads.
+//
+// Within a K step the MFMA sub-step s (0..15) takes k = 16 h + s from lane half h = lane / 32 in
+// both operands (any k order is valid when A and B agree), so a lane's A values for 4 sub-steps
+// are 4 consecutive k of one row: one ds_read_b128. The wave's 128 output columns are assigned
+// col = 4 (lane % 32) + j to accumulator tile j, so one ds_read_b128 of a B row serves the four
+// column tiles, and the epilogue writes 4 consecutive columns per lane.
+//
+// LDS layouts: A rows of 32 f32 (128 bytes), 16-byte chunk c of row r at chunk c ^ ((r / 2) % 8)
+// (16 consecutive rows of one read hit 16 distinct bank groups); B rows of 256 f32, unswizzled
+// (32 consecutive lanes read 512 contiguous bytes).
+//
+// C supplies M, N, K (multiples of 256, 256, 32), A_B, A_M (A is K-contiguous), B_B, B_K (B is
+// N-contiguous); the epilogue functor receives (batch, m, n, value).
+// ---------------------------------------------------------------------------------------------
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <class C>
+__device__ __forceinline__ void f32_issue(const float* __restrict__ Ab, const float* __restrict__ Bb, long m0, long n0,
+                                          long k0, float* as, float* bs, int wave, int lane) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int gi = wave * 8 + i;  // 1 KiB per instruction: 8 A rows, or 1 B row
+    const int row = 8 * gi + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    dma16(Ab + (m0 + row) * C::A_M + k0 + 4 * c, (ACCY_LDS void*)(as + gi * 256));
+    dma16(Bb + (k0 + gi) * C::B_K + n0 + 4 * lane, (ACCY_LDS void*)(bs + gi * 256));
+  }
+}
+
+template <class C, class Epi>
+__device__ __forceinline__ void mma32f(const float* __restrict__ A, const float* __restrict__ B, const Epi& epi) {
+  constexpr int BM = 256, BN = 256, BKF = 32;
+  constexpr long TILES_M = C::M / BM, TILES_N = C::N / BN, KT = C::K / BKF;
+  static_assert(C::M % BM == 0 && C::N % BN == 0 && C::K % BKF == 0, "exact tiles only");
+  __shared__ __attribute__((aligned(1024))) float a0[BM * BKF], a1[BM * BKF];
+  __shared__ __attribute__((aligned(1024))) float b0[BKF * BN], b1[BKF * BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1, h = lane >> 5, l32 = lane & 31;
+  long tm, tn;
+  tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
+  const long m0 = tm * BM, n0 = tn * BN, batch = blockIdx.y;
+  const float* __restrict__ Ab = A + batch * C::A_B;
+  const float* __restrict__ Bb = B + batch * C::B_B;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  auto step = [&](const float* as, const float* bs) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      f32x4 av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wm * 128 + i * 32 + l32;
+        const int pc = (4 * h + c) ^ ((row >> 1) & 7);
+        av[i] = *(const f32x4*)(as + row * BKF + pc * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) bv[u] = *(const f32x4*)(bs + (16 * h + 4 * c + u) * BN + wn * 128 + 4 * l32);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[i][j] = mfma32x32x2f32(av[i][u], bv[u][j], acc[i][j]);
+    }
+  };
+
+  f32_issue<C>(Ab, Bb, m0, n0, 0, a0, b0, wave, lane);
+  long kt = 0;
+  for (; kt + 2 <= KT; kt += 2) {
+    wait_vmcnt<0>();
+    lds_reads_done_barrier();
+    if (kt + 1 < KT) f32_issue<C>(Ab, Bb, m0, n0, (kt + 1) * BKF, a1, b1, wave, lane);
+    step(a0, b0);
+    wait_vmcnt<0>();
+    lds_reads_done_barrier();
+    if (kt + 2 < KT) f32_issue<C>(Ab, Bb, m0, n0, (kt + 2) * BKF, a0, b0, wave, lane);
+    step(a1, b1);
+  }
+  if (kt < KT) {
+    wait_vmcnt<0>();
+    lds_reads_done_barrier();
+    step(a0, b0);
+  }
+
+  const long col_base = n0 + wn * 128 + 4 * l32;
+  const long row_base = m0 + wm * 128 + 4 * h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) epi(batch, row_base + i * 32 + g * 8 + r, col_base + j, acc[i][j][g * 4 + r]);
+}
+
 }  // namespace gemm
 }  // namespace accy

@@ -64,3 +64,18 @@ extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_nn(const u
 extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_tn(const u16_t* a, const u16_t* b, u16_t* c) {
   accy::gemm::mma16_dma<CheckDmaTN>(a, b, CheckEpi{c, 128});
 }
+
+struct CheckF32NN {
+  static constexpr long M = 8192, N = 8192, K = 8192;
+  static constexpr long A_B = 0, A_M = 8192, B_B = 0, B_K = 8192;
+};
+
+struct CheckEpiF32 {
+  float* c;
+  long ld;
+  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const { c[m * ld + n] = v; }
+};
+
+extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_f32_nn(const float* a, const float* b, float* c) {
+  accy::gemm::mma32f<CheckF32NN>(a, b, CheckEpiF32{c, 8192});
+}

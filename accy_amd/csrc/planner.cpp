@@ -148,7 +148,7 @@ class Planner {
     switch (op.kind) {
       case Kind::parameter: break;
       case Kind::reduce:
-        if (!row_group(v)) fold(v);
+        if (!mulsum(v) && !row_group(v)) fold(v);
         break;
       case Kind::dot_general: dot(v); break;
       case Kind::scatter_add: scatter_add(v); break;
@@ -658,9 +658,16 @@ class Planner {
   bool gemm_eligible(const Op& op, GemmShape& gs) const {
     if (!opt_.allow_gemm) return false;
     DType d = op.result.dtype;
-    if (d != DType::bf16 && d != DType::f16) return false;
+    if (d != DType::bf16 && d != DType::f16 && d != DType::f32) return false;
     if (!gemm_shape(op, gs)) return false;
     if (gs.m * gs.n * gs.k == 0) return false;
+    if (d == DType::f32) {
+      // The f32 MFMA kernel: exact 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with
+      // 16-byte aligned rows; other f32 contractions keep runCpu's serial k order.
+      auto ok4 = [](int64_t x) { return x % 4 == 0; };
+      return gs.m % 256 == 0 && gs.n % 256 == 0 && gs.k % 32 == 0 && gs.a_k == 1 && gs.b_n == 1 && ok4(gs.a_m) &&
+             ok4(gs.b_k) && ok4(gs.a_b) && ok4(gs.b_b) && ok4(gs.a.offset) && ok4(gs.b.offset);
+    }
     auto ok8 = [](int64_t v) { return v % 8 == 0; };
     bool a_kc = gs.a_k == 1 && ok8(gs.k) && (gs.m == 1 || ok8(gs.a_m));
     bool a_mc = gs.a_m == 1 && ok8(gs.m) && (gs.k == 1 || ok8(gs.a_k));
@@ -677,7 +684,7 @@ class Planner {
     for (uint32_t v = 0; v < g_.ops.size(); ++v) {
       const Op& op = g_.ops[v];
       if (!live_[v] || op.kind != Kind::dot_general || attn_.count(v)) continue;
-      if (op.result.dtype != DType::bf16 && op.result.dtype != DType::f16) continue;
+      if (op.result.dtype != DType::bf16 && op.result.dtype != DType::f16 && op.result.dtype != DType::f32) continue;
       for (uint32_t a : op.args) {
         if (!view_chain_to_anchor(a)) needed_[a] = true;
       }
@@ -967,9 +974,15 @@ class Planner {
         << "; }\n"
         << "  static __device__ __forceinline__ long v_off(long b) { return " << batch_offset(L.extents, L.v_b, L.v.offset)
         << "; }\n};\n";
-    src << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << nm << "(const u16_t* __restrict__ "
-        << q << ", const u16_t* __restrict__ " << k << ", const u16_t* __restrict__ " << v << ", u16_t* __restrict__ "
-        << o << ") {\n  accy::attn::flash<Cfg_" << nm << ">(" << q << ", " << k << ", " << v << ", " << o << ");\n}\n";
+    // One parameter per distinct buffer (Q, K and V may share one).
+    std::string params;
+    for (const std::string& x : {q, k, v}) {
+      if (params.find("* __restrict__ " + x + ",") != std::string::npos) continue;
+      params += "const u16_t* __restrict__ " + x + ", ";
+    }
+    params += "u16_t* __restrict__ " + o;
+    src << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << nm << "(" << params
+        << ") {\n  accy::attn::flash<Cfg_" << nm << ">(" << q << ", " << k << ", " << v << ", " << o << ");\n}\n";
     KernelStep ks;
     ks.source = src.str();
     ks.name = nm;
@@ -1013,68 +1026,225 @@ class Planner {
     dot_serial(v);
   }
 
+  // Output layout of a contraction result: strides of the flattened batch, m and n groups.
+  struct OutStrides {
+    int64_t b = 0, m = 0, n = 1;
+  };
+
   void gemm(uint32_t v, const GemmShape& gs) {
+    OutStrides os;
+    os.b = gs.m * gs.n;
+    os.m = gs.n;
+    os.n = 1;
+    gemm(v, gs, os);
+  }
+
+  // Writes the contraction described by gs into the slot of value v (laid out per os).
+  void gemm(uint32_t v, const GemmShape& gs, const OutStrides& os) {
     const Op& op = g_.ops[v];
     int out = slots_.slot_of[v] >= 0 ? slots_.slot_of[v] : temp_slot(v);
     DType d = op.result.dtype;
-    // 256 x 256 x 64 tiles; the wave grid (4 x 2 waves of 64 x 128, or 2 x 2 waves of 128 x 128)
-    // can be overridden with ACCY_GEMM_WAVES=MxN for tuning.
-    const int BM = 256, BN = 256, BK = 64;
-    int WM = 2, WN = 2;
-    if (const char* s = std::getenv("ACCY_GEMM_WAVES")) {
-      int m = 0, n = 0;
-      if (std::sscanf(s, "%dx%d", &m, &n) == 2 && (m == 2 || m == 4) && (n == 2 || n == 4) && m * n <= 8) {
-        WM = m;
-        WN = n;
-      }
-    }
-    // Direct-to-LDS pipeline when the tiles divide the problem exactly (every row start 16-byte
-    // aligned); otherwise the register-staged kernel, which guards edges.
-    int dm = gs.m % 256 == 0 ? 256 : (gs.m % 128 == 0 ? 128 : 0);
-    int dn = gs.n % 256 == 0 ? 256 : (gs.n % 128 == 0 ? 128 : 0);
-    bool a_ok = (gs.a_k == 1 && gs.a_m % 8 == 0) || (gs.a_m == 1 && gs.a_k % 8 == 0);
-    bool b_ok = (gs.b_k == 1 && gs.b_n % 8 == 0) || (gs.b_n == 1 && gs.b_k % 8 == 0);
-    bool dma = dm && dn && gs.k % 128 == 0 && a_ok && b_ok && !std::getenv("ACCY_GEMM_NO_DMA");
     KernelWriter w(g_, slots_, "i64_t");
     std::string a = w.arg(gs.a.slot, false), b = w.arg(gs.b.slot, false), c = w.arg(out, true);
     std::string nm = name("gemm", v);
     std::ostringstream src;
-    src << "#include \"gemm\"\n";
-    src << "struct Cfg_" << nm << " {\n"
-        << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
-        << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
-        << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", A_K = " << gs.a_k << ";\n"
-        << "  static constexpr long B_B = " << gs.b_b << ", B_K = " << gs.b_k << ", B_N = " << gs.b_n << ";\n"
-        << "  static constexpr bool A_KC = " << (gs.a_k == 1 ? "true" : "false")
-        << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n";
-    if (dma) {
-      src << "  static constexpr int BM = " << dm << ", BN = " << dn << ";\n};\n";
-    } else {
-      src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
-          << ", WAVES_N = " << WN << ";\n};\n";
-    }
-    src << "struct Epi_" << nm << " {\n  u16_t* __restrict__ c;\n"
-        << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
-        << "    c[b * " << gs.m * gs.n << "L + m * " << gs.n << "L + n] = accy::f32_to_"
-        << (d == DType::bf16 ? "bf16" : "f16") << "(v);\n  }\n};\n";
-    int threads = dma ? 256 : WM * WN * 64;
-    src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(const u16_t* __restrict__ "
-        << a << ", const u16_t* __restrict__ " << b << ", u16_t* __restrict__ " << c << ") {\n"
-        << "  accy::gemm::" << (dma ? "mma16_dma" : "mma16") << "<Cfg_" << nm << ">(" << a << " + " << gs.a.offset
-        << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
     KernelStep k;
+    // One parameter per distinct buffer (both operands may be the same buffer).
+    const char* et = d == DType::f32 ? "float" : "u16_t";
+    std::string params = std::string("const ") + et + "* __restrict__ " + a;
+    if (b != a) params += std::string(", const ") + et + "* __restrict__ " + b;
+    params += std::string(", ") + et + "* __restrict__ " + c;
+    const std::string cidx = "b * " + std::to_string(os.b) + "L + m * " + std::to_string(os.m) + "L + n * " +
+                             std::to_string(os.n) + "L";
+    if (d == DType::f32) {
+      // f32 on v_mfma_f32_32x32x2_f32: exact 256 x 256 x 32 tiles (gemm_eligible checked the layout).
+      src << "#include \"gemm\"\n";
+      src << "struct Cfg_" << nm << " {\n"
+          << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
+          << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", B_B = " << gs.b_b
+          << ", B_K = " << gs.b_k << ";\n};\n";
+      src << "struct Epi_" << nm << " {\n  float* __restrict__ c;\n"
+          << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const { c[" << cidx
+          << "] = v; }\n};\n";
+      src << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << params << ") {\n"
+          << "  accy::gemm::mma32f<Cfg_" << nm << ">(" << a << " + " << gs.a.offset << "L, " << b << " + "
+          << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
+      k.grid[0] = (uint32_t)((gs.m / 256) * (gs.n / 256));
+      k.block[0] = 256;
+    } else {
+      // 256 x 256 x 64 tiles; the wave grid (4 x 2 waves of 64 x 128, or 2 x 2 waves of 128 x 128)
+      // can be overridden with ACCY_GEMM_WAVES=MxN for tuning.
+      const int BM = 256, BN = 256, BK = 64;
+      int WM = 2, WN = 2;
+      if (const char* e = std::getenv("ACCY_GEMM_WAVES")) {
+        int m = 0, n = 0;
+        if (std::sscanf(e, "%dx%d", &m, &n) == 2 && (m == 2 || m == 4) && (n == 2 || n == 4) && m * n <= 8) {
+          WM = m;
+          WN = n;
+        }
+      }
+      // Direct-to-LDS pipeline when the tiles divide the problem exactly (every row start 16-byte
+      // aligned); otherwise the register-staged kernel, which guards edges.
+      int dm = gs.m % 256 == 0 ? 256 : (gs.m % 128 == 0 ? 128 : 0);
+      int dn = gs.n % 256 == 0 ? 256 : (gs.n % 128 == 0 ? 128 : 0);
+      bool a_ok = (gs.a_k == 1 && gs.a_m % 8 == 0) || (gs.a_m == 1 && gs.a_k % 8 == 0);
+      bool b_ok = (gs.b_k == 1 && gs.b_n % 8 == 0) || (gs.b_n == 1 && gs.b_k % 8 == 0);
+      bool dma = dm && dn && gs.k % 128 == 0 && a_ok && b_ok && !std::getenv("ACCY_GEMM_NO_DMA");
+      src << "#include \"gemm\"\n";
+      src << "struct Cfg_" << nm << " {\n"
+          << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
+          << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
+          << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", A_K = " << gs.a_k << ";\n"
+          << "  static constexpr long B_B = " << gs.b_b << ", B_K = " << gs.b_k << ", B_N = " << gs.b_n << ";\n"
+          << "  static constexpr bool A_KC = " << (gs.a_k == 1 ? "true" : "false")
+          << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n";
+      if (dma) {
+        src << "  static constexpr int BM = " << dm << ", BN = " << dn << ";\n};\n";
+      } else {
+        src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
+            << ", WAVES_N = " << WN << ";\n};\n";
+      }
+      src << "struct Epi_" << nm << " {\n  u16_t* __restrict__ c;\n"
+          << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
+          << "    c[" << cidx << "] = accy::f32_to_" << (d == DType::bf16 ? "bf16" : "f16") << "(v);\n  }\n};\n";
+      int threads = dma ? 256 : WM * WN * 64;
+      src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(" << params << ") {\n"
+          << "  accy::gemm::" << (dma ? "mma16_dma" : "mma16") << "<Cfg_" << nm << ">(" << a << " + " << gs.a.offset
+          << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
+      int64_t tiles = dma ? (gs.m / dm) * (gs.n / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
+      k.grid[0] = (uint32_t)tiles;
+      k.block[0] = threads;
+      k.shared_bytes = dma ? 0u : 2u * (BM + BN) * (BK + 8) * 2u;
+    }
     k.source = src.str();
     k.name = nm;
-    int64_t tiles = dma ? (gs.m / dm) * (gs.n / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
-    k.grid[0] = (uint32_t)tiles;
     k.grid[1] = (uint32_t)gs.batch;
-    k.block[0] = threads;
-    k.shared_bytes = dma ? 0u : 2u * (BM + BN) * (BK + 8) * 2u;
     k.klass = "gemm";
     k.label = "gemm:%" + std::to_string(v);
     k.algorithmic_flops = 2.0 * (double)gs.batch * (double)gs.m * (double)gs.n * (double)gs.k;
     push(std::move(k), w);
     finish(v);
+  }
+
+  // ---- sum over k of mul(A, B): the same contraction, spelled elementwise ----
+  //
+  // reduce_sum_K(mul(broadcast_in_dim(A), broadcast_in_dim(B))) where every reduced axis comes from
+  // both A and B is dot_general(A, B) with those axes contracted, the kept axes of both as batch
+  // axes and the rest free. runCpu rounds each product to the element type before summing; the
+  // matrix cores form exact products (a difference inside the contraction tolerances), so this is
+  // used only where the MFMA kernels apply.
+  struct Operand {
+    uint32_t src = 0;
+    std::vector<int> to_mul;  // per source dim: the mul dim it becomes
+  };
+
+  bool operand_of(uint32_t u, size_t rank, Operand& o) const {
+    const Op& op = g_.ops[u];
+    if (op.kind == Kind::broadcast_in_dim) {
+      o.src = op.args[0];
+      o.to_mul.assign(op.ints.begin(), op.ints.end());
+    } else {
+      if (op.result.rank() != rank) return false;
+      o.src = u;
+      o.to_mul.resize(rank);
+      for (size_t i = 0; i < rank; ++i) o.to_mul[i] = (int)i;
+    }
+    return true;
+  }
+
+  bool mulsum(uint32_t v) {
+    const Op& red = g_.ops[v];
+    if ((Reducer)red.code != Reducer::sum) return false;
+    const DType d = red.result.dtype;
+    if (d != DType::f32 && d != DType::bf16 && d != DType::f16) return false;
+    double init;
+    if (!splat_float(red.args[1], init) || init != 0.0) return false;
+    const Op& mul = g_.ops[red.args[0]];
+    if (mul.kind != Kind::binary || (Binary)mul.code != Binary::mul || mul.result.dtype != d) return false;
+    const Type& mt = mul.result;
+    const size_t R = mt.rank();
+    Operand A, B;
+    if (!operand_of(mul.args[0], R, A) || !operand_of(mul.args[1], R, B)) return false;
+    // For each mul dim: the A / B source dim that supplies it (-1 if broadcast there).
+    std::vector<int> from_a(R, -1), from_b(R, -1);
+    const Type& at = g_.type(A.src);
+    const Type& bt = g_.type(B.src);
+    for (size_t i = 0; i < A.to_mul.size(); ++i)
+      if (at.dims[i].extent == mt.dims[(size_t)A.to_mul[i]].extent && at.dims[i].extent != 1) from_a[(size_t)A.to_mul[i]] = (int)i;
+    for (size_t i = 0; i < B.to_mul.size(); ++i)
+      if (bt.dims[i].extent == mt.dims[(size_t)B.to_mul[i]].extent && bt.dims[i].extent != 1) from_b[(size_t)B.to_mul[i]] = (int)i;
+    std::vector<bool> reduced(R, false);
+    for (int64_t a : red.ints) reduced[(size_t)a] = true;
+    Op dot;
+    dot.kind = Kind::dot_general;
+    dot.args = {A.src, B.src};
+    std::vector<Dim> batch_dims, lf_dims, rf_dims;
+    std::vector<size_t> batch_mul, lf_mul, rf_mul;
+    for (size_t i = 0; i < R; ++i) {
+      if (mt.dims[i].extent == 1) {
+        // Size-one axes: must not come from a real axis of both (nothing to contract or batch).
+        continue;
+      }
+      const bool ia = from_a[i] >= 0, ib = from_b[i] >= 0;
+      if (reduced[i]) {
+        if (!ia || !ib) return false;
+        dot.lhs_contract.push_back(from_a[i]);
+        dot.rhs_contract.push_back(from_b[i]);
+      } else if (ia && ib) {
+        dot.lhs_batch.push_back(from_a[i]);
+        dot.rhs_batch.push_back(from_b[i]);
+        batch_dims.push_back(mt.dims[i]);
+        batch_mul.push_back(i);
+      } else if (ia) {
+        lf_dims.push_back(mt.dims[i]);
+        lf_mul.push_back(i);
+      } else if (ib) {
+        rf_dims.push_back(mt.dims[i]);
+        rf_mul.push_back(i);
+      } else {
+        return false;
+      }
+    }
+    // Source dims that are not used (size one, or broadcast away) must have extent one.
+    auto covered = [](const std::vector<int>& from, size_t src_dim) {
+      return std::find(from.begin(), from.end(), (int)src_dim) != from.end();
+    };
+    for (size_t i = 0; i < at.rank(); ++i)
+      if (!covered(from_a, i) && at.dims[i].extent != 1) return false;
+    for (size_t i = 0; i < bt.rank(); ++i)
+      if (!covered(from_b, i) && bt.dims[i].extent != 1) return false;
+    // The contraction's free dims must flatten in the order the sources hold them; the dot result
+    // is [batch, lhs free, rhs free].
+    dot.result.dtype = d;
+    for (auto* g : {&batch_dims, &lf_dims, &rf_dims})
+      for (const Dim& x : *g) dot.result.dims.push_back(x);
+    if (dot.lhs_contract.empty()) return false;
+    GemmShape gs;
+    if (!gemm_eligible(dot, gs)) return false;
+    // Matrix cores only pay when both output extents fill a tile; x * x summed over an axis (a
+    // norm) stays a row reduction.
+    if (gs.m < 32 || gs.n < 32) return false;
+    // Output strides: the reduce result keeps the non-reduced mul dims in order.
+    std::vector<int64_t> rstr = row_major_strides(red.result.dims);
+    std::vector<int> res_pos(R, -1);
+    for (size_t i = 0, r = 0; i < R; ++i)
+      if (!reduced[i]) res_pos[i] = (int)r++;
+    auto group = [&](const std::vector<size_t>& muls, int64_t& extent, int64_t& stride) {
+      std::vector<Dim> dims;
+      std::vector<int64_t> strides;
+      std::vector<size_t> idx;
+      for (size_t j = 0; j < muls.size(); ++j) {
+        dims.push_back(mt.dims[muls[j]]);
+        strides.push_back(rstr[(size_t)res_pos[muls[j]]]);
+        idx.push_back(j);
+      }
+      return flatten(dims, strides, idx, extent, stride);
+    };
+    OutStrides os;
+    int64_t e;
+    if (!group(batch_mul, e, os.b) || !group(lf_mul, e, os.m) || !group(rf_mul, e, os.n)) return false;
+    gemm(v, gs, os);
+    return true;
   }
 
   // ---- dot_general with runCpu's per-output serial k order ----

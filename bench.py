@@ -56,17 +56,17 @@ def config_table():
                             4096 * 8192 * 4 + 4096 * 4),
             sample_desc="4096 of 32768 rows x 8192 features", workload=dict(rows=32768, features=8192)),
         "c3-gemm-f32": dict(
-            make=lambda: (W.gemm_program(8192, 8192, 8192, "f32"), W.gemm_inputs(8192, 8192, 8192, "f32")),
+            make=lambda: (W.gemm_program(8192, 8192, 8192, "f32", "mulsum"), W.gemm_inputs(8192, 8192, 8192, "f32")),
             dtype="f32", unit="TFLOP/s", bound="mfma", work=2.0 * 8192 ** 3, peak=MFMA_PEAK_TFLOPS["f32"],
-            sample=lambda: (W.gemm_program(16, 8192, 8192, "f32"), W.gemm_inputs(16, 8192, 8192, "f32"),
+            sample=lambda: (W.gemm_program(16, 8192, 8192, "f32", "mulsum"), W.gemm_inputs(16, 8192, 8192, "f32"),
                             2.0 * 16 * 8192 * 8192),
-            sample_desc="16 of 8192 rows of A", workload=dict(m=8192, k=8192, n=8192)),
+            sample_desc="16 of 8192 rows of A", workload=dict(m=8192, k=8192, n=8192, spelling="mul+sum")),
         "c3-gemm-bf16": dict(
-            make=lambda: (W.gemm_program(8192, 8192, 8192, "bf16"), W.gemm_inputs(8192, 8192, 8192, "bf16")),
+            make=lambda: (W.gemm_program(8192, 8192, 8192, "bf16", "mulsum"), W.gemm_inputs(8192, 8192, 8192, "bf16")),
             dtype="bf16", unit="TFLOP/s", bound="mfma", work=2.0 * 8192 ** 3, peak=MFMA_PEAK_TFLOPS["bf16"],
-            sample=lambda: (W.gemm_program(16, 8192, 8192, "bf16"), W.gemm_inputs(16, 8192, 8192, "bf16"),
+            sample=lambda: (W.gemm_program(16, 8192, 8192, "bf16", "mulsum"), W.gemm_inputs(16, 8192, 8192, "bf16"),
                             2.0 * 16 * 8192 * 8192),
-            sample_desc="16 of 8192 rows of A", workload=dict(m=8192, k=8192, n=8192)),
+            sample_desc="16 of 8192 rows of A", workload=dict(m=8192, k=8192, n=8192, spelling="mul+sum")),
         "c4-attention": dict(
             make=lambda: (W.attention_program(32, 4096, 128, "f16"), W.attention_inputs(32, 4096, 128, "f16")),
             dtype="f16", unit="TFLOP/s", bound="mfma", work=4.0 * 32 * 4096 * 4096 * 128,

@@ -150,9 +150,19 @@ def assert_attention(got, ref, tol, dtype, exact=None):
         assert mine <= 1.5 * theirs + ulp * np.abs(exact).max(), f"error vs exact {mine:.3e}, runCpu's {theirs:.3e}"
 
 
+def assert_no_less_accurate(got, ref, exact, dtype):
+    """max|got - exact| <= 1.5 max|runCpu - exact| + one 16-bit rounding of max|exact|: the result
+    is at least as close to the float64 value as runCpu's own per-op evaluation."""
+    g = to_f32(np.asarray(got), dtype).astype(np.float64)
+    r = to_f32(np.asarray(ref), dtype).astype(np.float64)
+    ulp = {"f16": 2.0 ** -10, "bf16": 2.0 ** -7}.get(dtype, 2.0 ** -23)
+    mine, theirs = np.abs(g - exact).max(), np.abs(r - exact).max()
+    assert mine <= 1.5 * theirs + ulp * np.abs(exact).max(), f"error vs exact {mine:.3e}, runCpu's {theirs:.3e}"
+
+
 def assert_normwise(got, ref, tol, dtype="f32", floor=1e-3):
     """GEMM / attention parity: max|g-r| / max|r| <= tol, and per element
-    |g-r| <= tol (|r| + floor max|r|)."""
+    |g-r| <= tol (|r| + floor max|r|) unless floor is None."""
     g = to_f32(np.asarray(got), dtype).astype(np.float64)
     r = to_f32(np.asarray(ref), dtype).astype(np.float64)
     scale = np.abs(r).max() if r.size else 0.0
@@ -160,6 +170,8 @@ def assert_normwise(got, ref, tol, dtype="f32", floor=1e-3):
     if r.size == 0:
         return
     assert err.max() <= tol * max(scale, 1e-30), f"normwise error {err.max() / max(scale, 1e-30):.3e} > {tol}"
+    if floor is None:
+        return
     bound = tol * (np.abs(r) + floor * scale)
     bad = err > bound
     assert not bad.any(), f"{bad.sum()} of {bad.size} elements beyond tol {tol} with floor {floor}"

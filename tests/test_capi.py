@@ -79,6 +79,31 @@ def test_attention_fusion_keeps_values_read_elsewhere():
     assert "accy::attn::flash" not in src
 
 
+@pytest.mark.parametrize("dtype,spelling,kernel", [
+    ("f32", "contract", "mma32f"), ("f32", "mulsum", "mma32f"),
+    ("bf16", "contract", "mma16_dma"), ("bf16", "mulsum", "mma16_dma")])
+def test_contractions_plan_onto_matrix_cores(dtype, spelling, kernel):
+    src = hip.plan_source(W.gemm_program(8192, 8192, 8192, dtype, spelling), compile=False)
+    assert ("accy::gemm::" + kernel + "<") in src
+    assert src.count("__global__") == 1
+
+
+def test_small_or_ragged_f32_contractions_keep_serial_order():
+    for m, k, n in [(33, 65, 17), (256, 30, 256), (300, 64, 256)]:
+        src = hip.plan_source(W.gemm_program(m, k, n, "f32", "mulsum"), compile=False)
+        assert "accy::gemm::" not in src
+
+
+def test_operands_sharing_one_buffer_compile():
+    # x . x^T on the matrix cores and self-attention with q = k = v: one kernel parameter each
+    gram = T.define("gram", [T.spec("bf16", m=256, k=128)],
+                    lambda b, a: a[0].contract(a[0].rename("m", "n"), "k"))
+    assert "accy::gemm::" in hip.plan_source(gram, compile=True)
+    specs = [T.spec("f16", head=2, query=128, dim=128)]
+    self_attn = T.define("self", specs, lambda b, a: W.attention_body("f16", 128)(b, [a[0], a[0], a[0]]))
+    assert "accy::attn::flash" in hip.plan_source(self_attn, compile=True)
+
+
 def test_indexing_and_integer_programs_compile():
     def body(b, a):
         g = a[0].gather(a[1], "v")

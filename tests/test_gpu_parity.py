@@ -14,8 +14,8 @@ import pytest
 from accy_amd import hip
 from accy_amd import tensor as T
 from accy_amd import workloads as W
-from conftest import (assert_attention, assert_normwise, assert_rel, exact_attention, hip_run, oracle_run,
-                      out_arrays, to_f32)
+from conftest import (assert_attention, assert_no_less_accurate, assert_normwise, assert_rel, exact_attention, hip_run,
+                      oracle_run, out_arrays, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -262,6 +262,67 @@ def test_gemm_direct_to_lds_layouts(case):
     src = hip.plan_source(prog)
     assert "mma16_dma" in src, src[:400]
     assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype)
+
+
+def _gemm_kernels(prog):
+    src = hip.plan_source(prog.encode(), compile=False)
+    return [l.split("accy::gemm::")[1].split("<")[0] for l in src.splitlines() if "accy::gemm::" in l]
+
+
+@pytest.mark.parametrize("m,k,n,spelling", [(512, 96, 256, "contract"), (256, 64, 512, "mulsum"),
+                                            (768, 32, 256, "mulsum"), (256, 8192, 256, "contract")])
+def test_gemm_f32_on_mfma(m, k, n, spelling):
+    say(f"gemm f32 {m}x{k}x{n} {spelling}")
+    prog = W.gemm_program(m, k, n, "f32", spelling)
+    assert _gemm_kernels(prog) == ["mma32f"]
+    ins = W.gemm_inputs(m, k, n, "f32", seed=m + k)
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-3, "f32")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_gemm_mulsum_16bit_on_mfma(dtype):
+    say(f"gemm {dtype} 256x256x512 mulsum")
+    prog = W.gemm_program(256, 256, 512, dtype, "mulsum")
+    assert _gemm_kernels(prog) == ["mma16_dma"]
+    ins = W.gemm_inputs(256, 256, 512, dtype, seed=12)
+    got, ref = hip_run(prog, ins)[0], oracle_run(prog, ins)[0]
+    # runCpu rounds every product to the 16-bit type before the f32 sum (the elementwise spelling);
+    # the matrix cores keep exact products. Near-zero sums therefore differ by runCpu's rounding
+    # noise (no per-element bound), and the result must be at least as close to the float64 product
+    # as runCpu's.
+    exact = to_f32(ins[0], dtype).astype(np.float64) @ to_f32(ins[1], dtype).astype(np.float64)
+    assert_normwise(got, ref, 2e-2, dtype, floor=None)
+    assert_no_less_accurate(got, ref, exact, dtype)
+
+
+def test_mulsum_batched_and_transposed_output():
+    say("mulsum batched f32 and [n, m] output bf16")
+    prog = T.define("bmm", [T.spec("f32", b=3, m=256, k=64), T.spec("f32", b=3, k=64, n=256)],
+                    lambda bb, a: a[0].mul(a[1]).sum("k"))
+    assert _gemm_kernels(prog) == ["mma32f"]
+    ins = [W.to_dtype(W.uniform(21, 3 * 256 * 64, -1, 1), "f32").reshape(3, 256, 64),
+           W.to_dtype(W.uniform(22, 3 * 64 * 256, -1, 1), "f32").reshape(3, 64, 256)]
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-3, "f32")
+    # B first: the traced union order is [k, n, m], so the result is [n, m] (transposed epilogue)
+    prog = T.define("nm", [T.spec("bf16", k=256, n=384), T.spec("bf16", m=128, k=256)],
+                    lambda bb, a: a[0].mul(a[1]).sum("k"))
+    assert _gemm_kernels(prog) in (["mma16"], ["mma16_dma"])
+    ins = [W.to_dtype(W.uniform(23, 256 * 384, -1, 1), "bf16").reshape(256, 384),
+           W.to_dtype(W.uniform(24, 128 * 256, -1, 1), "bf16").reshape(128, 256)]
+    got, ref = hip_run(prog, ins)[0], oracle_run(prog, ins)[0]
+    assert got.shape == (384, 128)
+    exact = (to_f32(ins[1], "bf16").astype(np.float64) @ to_f32(ins[0], "bf16").astype(np.float64)).T
+    assert_normwise(got, ref, 2e-2, "bf16", floor=None)
+    assert_no_less_accurate(got, ref, exact, "bf16")
+
+
+def test_gemm_f32_full_size_on_sampled_rows():
+    say("gemm f32 8192^3 mul+sum (full)")
+    a, b = W.gemm_inputs(8192, 8192, 8192, "f32")
+    got = hip_run(W.gemm_program(8192, 8192, 8192, "f32", "mulsum"), [a, b])[0]
+    rows = np.sort(np.random.default_rng(2).choice(8192, 8, replace=False))
+    ref = oracle_run(W.gemm_program(8, 8192, 8192, "f32", "mulsum"), [a[rows], b])[0]
+    assert_normwise(got[rows], ref, 1e-3, "f32")
 
 
 def test_gemm_bf16_full_size_on_sampled_rows():

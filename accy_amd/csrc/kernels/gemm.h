@@ -265,9 +265,34 @@ __device__ __forceinline__ void lds_reads_done_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Element offsets of an operand tile: O::row(i) of row (M or N) index i, O::k(i) of contraction
+// index i. The configuration struct supplies them as a_m / a_k / b_n / b_k (and a_b / b_b for the
+// batch index): plain products for strided operands, or sums over several axes when a named group
+// does not collapse to one stride. Within one tile the contiguous group is affine (the planner
+// checks that its innermost axis has stride 1 and a multiple of the tile as extent).
+template <class C> struct AOff {
+  static __device__ __forceinline__ long row(long i) { return C::a_m(i); }
+  static __device__ __forceinline__ long k(long i) { return C::a_k(i); }
+};
+template <class C> struct BOff {
+  static __device__ __forceinline__ long row(long i) { return C::b_n(i); }
+  static __device__ __forceinline__ long k(long i) { return C::b_k(i); }
+};
+
+// Offset functions of single-stride operands, for configurations written by hand.
+template <long AB, long AM, long AK, long BB, long BK, long BN>
+struct Strided {
+  static __device__ __forceinline__ long a_b(long i) { return i * AB; }
+  static __device__ __forceinline__ long a_m(long i) { return i * AM; }
+  static __device__ __forceinline__ long a_k(long i) { return i * AK; }
+  static __device__ __forceinline__ long b_b(long i) { return i * BB; }
+  static __device__ __forceinline__ long b_k(long i) { return i * BK; }
+  static __device__ __forceinline__ long b_n(long i) { return i * BN; }
+};
+
 // Issues load instruction i of this wave's share of one operand tile (ROWS * 64 bytes, 1 KiB per
 // wave instruction, INSTRS / 4 instructions per wave). KC: rows of 32 k (64 bytes); else rows of k.
-template <int ROWS, bool KC, long SR, long SK>
+template <int ROWS, bool KC, class O>
 __device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave,
                                          int lane, int i) {
   constexpr int INSTRS = ROWS * 64 / 1024;
@@ -277,7 +302,7 @@ __device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0
   if constexpr (KC) {
     const int q = (lane & 7) ^ (lane >> 3);  // logical slot of this lane's physical chunk
     const int row = 16 * gi + 2 * (lane >> 3) + (q >> 2);
-    src = base + (r0 + row) * SR + k0 + 8 * (q & 3);
+    src = base + O::row(r0 + row) + O::k(k0) + 8 * (q & 3);
   } else {
     constexpr int ROWB = ROWS * 2;    // bytes per k row
     constexpr int LPR = ROWB / 16;    // lanes per k row
@@ -285,15 +310,15 @@ __device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0
     const int row = RPI * gi + lane / LPR;
     const int p = lane % LPR;
     const int u = (p >> 1) ^ (row & 7);
-    src = base + (k0 + row) * SK + r0 + 16 * u + 8 * (p & 1);
+    src = base + O::k(k0 + row) + O::row(r0) + 16 * u + 8 * (p & 1);
   }
   dma16(src, (ACCY_LDS void*)(lds + gi * 512));
 }
 
-template <int ROWS, bool KC, long SR, long SK>
+template <int ROWS, bool KC, class O>
 __device__ __forceinline__ void dma_tile(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < ROWS * 64 / 1024 / 4; ++i) dma_part<ROWS, KC, SR, SK>(base, r0, k0, lds, wave, lane, i);
+  for (int i = 0; i < ROWS * 64 / 1024 / 4; ++i) dma_part<ROWS, KC, O>(base, r0, k0, lds, wave, lane, i);
 }
 
 // Fragment of 32 rows (M or N) x 16 k for one MFMA, read from a stage.
@@ -369,9 +394,9 @@ struct DmaStep {
         if (k < NF) {
           f1.load_one(k, as[STAGE], bs[STAGE], 1, lane, wm, wn);
         } else if (k - NF < DA) {
-          dma_part<C::BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, (kt + 3) * 32, as[NEXT], wave, lane, k - NF);
+          dma_part<C::BM, C::A_KC, AOff<C>>(Ab, m0, (kt + 3) * 32, as[NEXT], wave, lane, k - NF);
         } else {
-          dma_part<C::BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, (kt + 3) * 32, bs[NEXT], wave, lane, k - NF - DA);
+          dma_part<C::BN, C::B_KC, BOff<C>>(Bb, n0, (kt + 3) * 32, bs[NEXT], wave, lane, k - NF - DA);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -413,8 +438,8 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
   long tm, tn;
   tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
   const long m0 = tm * BM, n0 = tn * BN, batch = blockIdx.y;
-  const u16_t* __restrict__ Ab = A + batch * C::A_B;
-  const u16_t* __restrict__ Bb = B + batch * C::B_B;
+  const u16_t* __restrict__ Ab = A + C::a_b(batch);
+  const u16_t* __restrict__ Bb = B + C::b_b(batch);
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -424,8 +449,8 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
 
 #pragma unroll
   for (int s = 0; s < 3; ++s) {
-    dma_tile<BM, C::A_KC, C::A_M, C::A_K>(Ab, m0, s * 32, as[s], wave, lane);
-    dma_tile<BN, C::B_KC, C::B_N, C::B_K>(Bb, n0, s * 32, bs[s], wave, lane);
+    dma_tile<BM, C::A_KC, AOff<C>>(Ab, m0, s * 32, as[s], wave, lane);
+    dma_tile<BN, C::B_KC, BOff<C>>(Bb, n0, s * 32, bs[s], wave, lane);
   }
   // Tile 0 complete everywhere (tiles 1 and 2 may still be in flight), then its first sub-step.
   Frags<C> f0;
@@ -477,8 +502,9 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
 // (16 consecutive rows of one read hit 16 distinct bank groups); B rows of 256 f32, unswizzled
 // (32 consecutive lanes read 512 contiguous bytes).
 //
-// C supplies M, N, K (multiples of 256, 256, 32), A_B, A_M (A is K-contiguous), B_B, B_K (B is
-// N-contiguous); the epilogue functor receives (batch, m, n, value).
+// C supplies M, N, K (multiples of 256, 256, 32) and the offset functions a_b, a_m, a_k (A is
+// K-contiguous within each 32-wide k tile), b_b, b_k, b_n (B is N-contiguous within each 256-wide
+// n tile); the epilogue functor receives (batch, m, n, value).
 // ---------------------------------------------------------------------------------------------
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -495,8 +521,8 @@ __device__ __forceinline__ void f32_issue(const float* __restrict__ Ab, const fl
     const int gi = wave * 8 + i;  // 1 KiB per instruction: 8 A rows, or 1 B row
     const int row = 8 * gi + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
-    dma16(Ab + (m0 + row) * C::A_M + k0 + 4 * c, (ACCY_LDS void*)(as + gi * 256));
-    dma16(Bb + (k0 + gi) * C::B_K + n0 + 4 * lane, (ACCY_LDS void*)(bs + gi * 256));
+    dma16(Ab + C::a_m(m0 + row) + C::a_k(k0) + 4 * c, (ACCY_LDS void*)(as + gi * 256));
+    dma16(Bb + C::b_k(k0 + gi) + C::b_n(n0) + 4 * lane, (ACCY_LDS void*)(bs + gi * 256));
   }
 }
 
@@ -513,8 +539,8 @@ __device__ __forceinline__ void mma32f(const float* __restrict__ A, const float*
   long tm, tn;
   tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
   const long m0 = tm * BM, n0 = tn * BN, batch = blockIdx.y;
-  const float* __restrict__ Ab = A + batch * C::A_B;
-  const float* __restrict__ Bb = B + batch * C::B_B;
+  const float* __restrict__ Ab = A + C::a_b(batch);
+  const float* __restrict__ Bb = B + C::b_b(batch);
 
   f32x16 acc[4][4];
 #pragma unroll

@@ -41,7 +41,7 @@ extern "C" __global__ void __launch_bounds__(256) accy_check_common(const float*
   if (threadIdx.x == 0) y[blockIdx.x] = accy::round_bf16(v);
 }
 
-struct CheckDmaNN {
+struct CheckDmaNN : accy::gemm::Strided<0, 8192, 1, 0, 8192, 1> {
   static constexpr int DT = 0;
   static constexpr long M = 8192, N = 8192, K = 8192;
   static constexpr long A_B = 0, A_M = 8192, A_K = 1, B_B = 0, B_K = 8192, B_N = 1;
@@ -49,7 +49,7 @@ struct CheckDmaNN {
   static constexpr int BM = 256, BN = 256;
 };
 
-struct CheckDmaTN {
+struct CheckDmaTN : accy::gemm::Strided<0, 1, 384, 0, 1, 256> {
   static constexpr int DT = 1;
   static constexpr long M = 384, N = 128, K = 256;
   static constexpr long A_B = 0, A_M = 1, A_K = 384, B_B = 0, B_K = 1, B_N = 256;
@@ -65,7 +65,7 @@ extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_tn(const u
   accy::gemm::mma16_dma<CheckDmaTN>(a, b, CheckEpi{c, 128});
 }
 
-struct CheckF32NN {
+struct CheckF32NN : accy::gemm::Strided<0, 8192, 1, 0, 8192, 1> {
   static constexpr long M = 8192, N = 8192, K = 8192;
   static constexpr long A_B = 0, A_M = 8192, B_B = 0, B_K = 8192;
 };
@@ -78,4 +78,22 @@ struct CheckEpiF32 {
 
 extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_f32_nn(const float* a, const float* b, float* c) {
   accy::gemm::mma32f<CheckF32NN>(a, b, CheckEpiF32{c, 8192});
+}
+
+// A contraction over two named axes of a [batch, head, seq, hd] operand: rows (batch, seq), k (head, hd).
+struct CheckDmaMultiAxis {
+  static constexpr int DT = 0;
+  static constexpr long M = 8192, N = 2048, K = 2048;
+  static constexpr bool A_KC = true, B_KC = false;
+  static constexpr int BM = 256, BN = 256;
+  static __device__ __forceinline__ long a_b(long) { return 0; }
+  static __device__ __forceinline__ long a_m(long i) { return (i / 2048) * 4194304L + (i % 2048) * 128L; }
+  static __device__ __forceinline__ long a_k(long i) { return (i / 128) * 262144L + (i % 128); }
+  static __device__ __forceinline__ long b_b(long) { return 0; }
+  static __device__ __forceinline__ long b_k(long i) { return i * 2048L; }
+  static __device__ __forceinline__ long b_n(long i) { return i; }
+};
+
+extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_multi(const u16_t* a, const u16_t* b, u16_t* c) {
+  accy::gemm::mma16_dma<CheckDmaMultiAxis>(a, b, CheckEpi{c, 2048});
 }

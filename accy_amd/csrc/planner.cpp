@@ -622,9 +622,62 @@ class Planner {
     return true;
   }
 
+  // The axes of one operand group (batch, rows or contraction) in the order that flattens the
+  // group's index, with their strides in the operand; neighbours that are contiguous are merged.
+  struct Group {
+    std::vector<int64_t> ext, str;  // runs, outermost first
+
+    static Group make(const std::vector<Dim>& dims, const std::vector<int64_t>& strides, const std::vector<size_t>& idx) {
+      Group g;
+      for (size_t d : idx) {
+        if (dims[d].extent == 1) continue;
+        if (!g.ext.empty() && g.str.back() == strides[d] * dims[d].extent) {
+          g.ext.back() *= dims[d].extent;
+          g.str.back() = strides[d];
+        } else {
+          g.ext.push_back(dims[d].extent);
+          g.str.push_back(strides[d]);
+        }
+      }
+      return g;
+    }
+    int64_t extent() const {
+      int64_t e = 1;
+      for (int64_t x : ext) e *= x;
+      return e;
+    }
+    bool single() const { return ext.size() <= 1; }
+    int64_t stride() const { return ext.empty() ? 0 : str[0]; }
+    // The innermost run: (extent, stride).
+    int64_t inner_ext() const { return ext.empty() ? 1 : ext.back(); }
+    int64_t inner_str() const { return ext.empty() ? 0 : str.back(); }
+    bool strides_multiple_of(int64_t q) const {
+      for (int64_t x : str)
+        if (x % q != 0) return false;
+      return true;
+    }
+    // Device function returning the element offset of flattened index i.
+    std::string fn(const std::string& name) const {
+      std::ostringstream s;
+      s << "  static __device__ __forceinline__ long " << name << "(long i) { return 0L";
+      int64_t inner = 1;
+      for (size_t r = ext.size(); r-- > 0;) {
+        s << " + ";
+        std::string idx = inner == 1 ? "i" : "(i / " + std::to_string(inner) + "L)";
+        if (r > 0) idx = "(" + idx + " % " + std::to_string(ext[r]) + "L)";
+        s << idx << " * " << str[r] << "L";
+        inner *= ext[r];
+      }
+      s << "; }\n";
+      return s.str();
+    }
+  };
+
   struct GemmShape {
     int64_t batch = 1, m = 1, n = 1, k = 1;
-    int64_t a_b = 0, a_m = 0, a_k = 0, b_b = 0, b_k = 0, b_n = 0;
+    int64_t a_b = 0, a_m = 0, a_k = 0, b_b = 0, b_k = 0, b_n = 0;  // single strides (when !multi)
+    Group ga_b, ga_m, ga_k, gb_b, gb_k, gb_n;
+    bool multi = false;
     View a, b;
   };
 
@@ -641,20 +694,73 @@ class Planner {
       if (!in(op.lhs_contract, i) && !in(op.lhs_batch, i)) lf.push_back(i);
     for (size_t i = 0; i < R.rank(); ++i)
       if (!in(op.rhs_contract, i) && !in(op.rhs_batch, i)) rf.push_back(i);
-    int64_t e2;
-    if (!flatten(L.dims, gs.a.strides, lb, gs.batch, gs.a_b)) return false;
-    if (!flatten(R.dims, gs.b.strides, rb, e2, gs.b_b) || e2 != gs.batch) return false;
-    if (!flatten(L.dims, gs.a.strides, lf, gs.m, gs.a_m)) return false;
-    if (!flatten(R.dims, gs.b.strides, rf, gs.n, gs.b_n)) return false;
-    if (!flatten(L.dims, gs.a.strides, lc, gs.k, gs.a_k)) return false;
-    if (!flatten(R.dims, gs.b.strides, rc, e2, gs.b_k) || e2 != gs.k) return false;
-    // Contraction axes must flatten in the same order on both sides: check pairwise extents.
+    // Batch and contraction axes pair up one to one.
     for (size_t i = 0; i < lc.size(); ++i)
       if (L.dims[lc[i]].extent != R.dims[rc[i]].extent) return false;
+    for (size_t i = 0; i < lb.size(); ++i)
+      if (L.dims[lb[i]].extent != R.dims[rb[i]].extent) return false;
+    // Size-one axes drop out; a batch or contraction axis of extent > 1 on one side only cannot be.
+    gs.ga_b = Group::make(L.dims, gs.a.strides, lb);
+    gs.gb_b = Group::make(R.dims, gs.b.strides, rb);
+    gs.ga_m = Group::make(L.dims, gs.a.strides, lf);
+    gs.gb_n = Group::make(R.dims, gs.b.strides, rf);
+    gs.ga_k = Group::make(L.dims, gs.a.strides, lc);
+    gs.gb_k = Group::make(R.dims, gs.b.strides, rc);
+    gs.batch = gs.ga_b.extent();
+    gs.m = gs.ga_m.extent();
+    gs.n = gs.gb_n.extent();
+    gs.k = gs.ga_k.extent();
+    if (gs.gb_b.extent() != gs.batch || gs.gb_k.extent() != gs.k) return false;
+    // Pairwise merging can differ between the two sides; the offset functions decompose the same
+    // flattened index either way, since merged runs are row-major over the same logical axes.
+    gs.multi = !(gs.ga_b.single() && gs.gb_b.single() && gs.ga_m.single() && gs.gb_n.single() && gs.ga_k.single() &&
+                 gs.gb_k.single());
+    gs.a_b = gs.ga_b.stride();
+    gs.b_b = gs.gb_b.stride();
+    gs.a_m = gs.ga_m.stride();
+    gs.b_n = gs.gb_n.stride();
+    gs.a_k = gs.ga_k.stride();
+    gs.b_k = gs.gb_k.stride();
     return true;
   }
 
-  // The MFMA template takes 16-bit operands whose K or M/N stride is 1, with 8-element aligned rows.
+  // Direct-to-LDS tile sizes for the 16-bit kernel (0: not applicable).
+  static int dma_rows(int64_t extent) { return extent % 256 == 0 ? 256 : (extent % 128 == 0 ? 128 : 0); }
+
+  // Operand layouts the direct-to-LDS kernel can stage: K-contiguous (the innermost contraction run
+  // has stride 1 and whole 32-wide k tiles) or row-contiguous (the innermost row run has stride 1
+  // and whole row tiles); every other stride and the offset 16-byte aligned.
+  static bool dma_operand(const Group& rows, const Group& k, const Group& batch, int64_t offset, int tile, bool& kc) {
+    if (!rows.strides_multiple_of(1) || offset % 8 != 0) return false;
+    auto aligned8 = [](const Group& g, bool skip_inner) {
+      for (size_t i = 0; i < g.str.size(); ++i) {
+        if (skip_inner && i + 1 == g.str.size()) continue;
+        if (g.str[i] % 8 != 0) return false;
+      }
+      return true;
+    };
+    if (!aligned8(batch, false)) return false;
+    if (k.inner_str() == 1 && k.inner_ext() % 32 == 0 && aligned8(k, true) && aligned8(rows, false)) {
+      kc = true;
+      return true;
+    }
+    if (rows.inner_str() == 1 && rows.inner_ext() % tile == 0 && aligned8(rows, true) && aligned8(k, false)) {
+      kc = false;
+      return true;
+    }
+    return false;
+  }
+
+  bool dma_eligible(const GemmShape& gs, int& dm, int& dn, bool& a_kc, bool& b_kc) const {
+    dm = dma_rows(gs.m);
+    dn = dma_rows(gs.n);
+    if (!dm || !dn || gs.k % 128 != 0 || std::getenv("ACCY_GEMM_NO_DMA")) return false;
+    return dma_operand(gs.ga_m, gs.ga_k, gs.ga_b, gs.a.offset, dm, a_kc) &&
+           dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, dn, b_kc);
+  }
+
+  // The MFMA templates take 16-bit operands whose K or M/N stride is 1, with 8-element aligned rows
+  // (or, for operands whose groups span several axes, the direct-to-LDS kernel's layouts).
   bool gemm_eligible(const Op& op, GemmShape& gs) const {
     if (!opt_.allow_gemm) return false;
     DType d = op.result.dtype;
@@ -665,8 +771,13 @@ class Planner {
       // The f32 MFMA kernel: exact 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with
       // 16-byte aligned rows; other f32 contractions keep runCpu's serial k order.
       auto ok4 = [](int64_t x) { return x % 4 == 0; };
-      return gs.m % 256 == 0 && gs.n % 256 == 0 && gs.k % 32 == 0 && gs.a_k == 1 && gs.b_n == 1 && ok4(gs.a_m) &&
-             ok4(gs.b_k) && ok4(gs.a_b) && ok4(gs.b_b) && ok4(gs.a.offset) && ok4(gs.b.offset);
+      return !gs.multi && gs.m % 256 == 0 && gs.n % 256 == 0 && gs.k % 32 == 0 && gs.a_k == 1 && gs.b_n == 1 &&
+             ok4(gs.a_m) && ok4(gs.b_k) && ok4(gs.a_b) && ok4(gs.b_b) && ok4(gs.a.offset) && ok4(gs.b.offset);
+    }
+    if (gs.multi) {
+      int dm, dn;
+      bool akc, bkc;
+      return dma_eligible(gs, dm, dn, akc, bkc);
     }
     auto ok8 = [](int64_t v) { return v % 8 == 0; };
     bool a_kc = gs.a_k == 1 && ok8(gs.k) && (gs.m == 1 || ok8(gs.a_m));
@@ -1061,8 +1172,8 @@ class Planner {
       src << "#include \"gemm\"\n";
       src << "struct Cfg_" << nm << " {\n"
           << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
-          << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", B_B = " << gs.b_b
-          << ", B_K = " << gs.b_k << ";\n};\n";
+          << gs.ga_b.fn("a_b") << gs.ga_m.fn("a_m") << gs.ga_k.fn("a_k") << gs.gb_b.fn("b_b") << gs.gb_k.fn("b_k")
+          << gs.gb_n.fn("b_n") << "};\n";
       src << "struct Epi_" << nm << " {\n  float* __restrict__ c;\n"
           << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const { c[" << cidx
           << "] = v; }\n};\n";
@@ -1084,20 +1195,20 @@ class Planner {
         }
       }
       // Direct-to-LDS pipeline when the tiles divide the problem exactly (every row start 16-byte
-      // aligned); otherwise the register-staged kernel, which guards edges.
-      int dm = gs.m % 256 == 0 ? 256 : (gs.m % 128 == 0 ? 128 : 0);
-      int dn = gs.n % 256 == 0 ? 256 : (gs.n % 128 == 0 ? 128 : 0);
-      bool a_ok = (gs.a_k == 1 && gs.a_m % 8 == 0) || (gs.a_m == 1 && gs.a_k % 8 == 0);
-      bool b_ok = (gs.b_k == 1 && gs.b_n % 8 == 0) || (gs.b_n == 1 && gs.b_k % 8 == 0);
-      bool dma = dm && dn && gs.k % 128 == 0 && a_ok && b_ok && !std::getenv("ACCY_GEMM_NO_DMA");
+      // aligned); otherwise the register-staged kernel, which guards edges (single strides only).
+      int dm = 0, dn = 0;
+      bool akc = gs.a_k == 1, bkc = gs.b_k == 1;
+      bool dma = dma_eligible(gs, dm, dn, akc, bkc);
       src << "#include \"gemm\"\n";
       src << "struct Cfg_" << nm << " {\n"
           << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
           << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
           << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", A_K = " << gs.a_k << ";\n"
           << "  static constexpr long B_B = " << gs.b_b << ", B_K = " << gs.b_k << ", B_N = " << gs.b_n << ";\n"
-          << "  static constexpr bool A_KC = " << (gs.a_k == 1 ? "true" : "false")
-          << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n";
+          << "  static constexpr bool A_KC = " << (akc ? "true" : "false") << ", B_KC = " << (bkc ? "true" : "false")
+          << ";\n"
+          << gs.ga_b.fn("a_b") << gs.ga_m.fn("a_m") << gs.ga_k.fn("a_k") << gs.gb_b.fn("b_b") << gs.gb_k.fn("b_k")
+          << gs.gb_n.fn("b_n");
       if (dma) {
         src << "  static constexpr int BM = " << dm << ", BN = " << dn << ";\n};\n";
       } else {

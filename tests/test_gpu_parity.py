@@ -14,8 +14,8 @@ import pytest
 from accy_amd import hip
 from accy_amd import tensor as T
 from accy_amd import workloads as W
-from conftest import (assert_attention, assert_no_less_accurate, assert_normwise, assert_rel, exact_attention, hip_run,
-                      oracle_run, out_arrays, to_f32)
+from conftest import (assert_attention, assert_no_less_accurate, assert_normwise, assert_rel, assert_rowwise,
+                      exact_attention, hip_run, oracle_run, out_arrays, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -323,6 +323,35 @@ def test_gemm_f32_full_size_on_sampled_rows():
     rows = np.sort(np.random.default_rng(2).choice(8192, 8, replace=False))
     ref = oracle_run(W.gemm_program(8, 8192, 8192, "f32", "mulsum"), [a[rows], b])[0]
     assert_normwise(got[rows], ref, 1e-3, "f32")
+
+
+def test_contraction_over_two_named_axes_on_mfma():
+    """o [batch, head, seq, hd] . w [head, hd, model] over (head, hd): both the rows (batch, seq) and
+    the contraction (head, hd) span two axes with separate strides (the decoder's out-projection)."""
+    say("contraction over (head, hd), rows over (batch, seq)")
+    specs = [T.spec("bf16", batch=2, head=4, seq=128, hd=128), T.spec("bf16", head=4, hd=128, model=256)]
+    prog = T.define("proj", specs, lambda b, a: a[0].contract(a[1], ("head", "hd")))
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "mma16_dma" in src and "(i / 128L)" in src
+    ins = [W.to_dtype(W.normal(31, 2 * 4 * 128 * 128), "bf16").reshape(2, 4, 128, 128),
+           W.to_dtype(0.05 * W.normal(32, 4 * 128 * 256), "bf16").reshape(4, 128, 256)]
+    got, ref = hip_run(prog, ins)[0], oracle_run(prog, ins)[0]
+    assert got.shape == (2, 128, 256)
+    assert_normwise(got, ref, 2e-2, "bf16")
+
+
+def test_decoder_full_size_on_one_batch_element():
+    """C5 at its full size. Batch elements are independent (attention mixes positions within one),
+    so the oracle runs the same block for one batch element of the same inputs."""
+    say("decoder 4 x 2048 x 2048, 16 x 128 heads, ffn 8192 (full)")
+    ins = W.decoder_inputs()
+    prog = W.decoder_program()
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "accy::attn::flash" in src and "accy_dot_" not in src
+    got = hip_run(prog, ins)[0]
+    b = 2
+    ref = oracle_run(W.decoder_program(batch=1), [ins[0][b:b + 1]] + ins[1:])[0]
+    assert_rowwise(got[b:b + 1], ref, 2e-2, "bf16")
 
 
 def test_gemm_bf16_full_size_on_sampled_rows():

@@ -56,6 +56,23 @@ __device__ __forceinline__ float exp_f32(float x) {
   return __builtin_ldexpf(__builtin_amdgcn_exp2f(f), (int)n);
 }
 
+// tanh: for |x| >= 1/8, 1 - 2 / (e^(2|x|) + 1) with e^(2|x|) from the hardware exp2 (v_exp_f32) and
+// the hardware reciprocal (v_rcp_f32), both about 1 ulp, so the result is within about 1e-6 relative
+// (the exp2 argument's rounding dominates near |x| = 1/8); below 1/8 the odd Taylor polynomial to
+// x^7 (truncation under 2e-9 relative), which avoids the cancellation of the first form. e = inf
+// gives 1; NaN propagates through the first form; the sign is copied back (tanh(-0) = -0). No
+// branches.
+__device__ __forceinline__ float tanh_f32(float x) {
+  const float ax = __builtin_fabsf(x);
+  const float e = __builtin_amdgcn_exp2f(ax * 0x1.715476p+1f);  // e^(2|x|)
+  const float big = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(e + 1.0f), 1.0f);
+  const float x2 = ax * ax;
+  float p = __builtin_fmaf(x2, -0x1.ba1ba2p-5f, 0x1.111112p-3f);  // -17/315, 2/15
+  p = __builtin_fmaf(x2, p, -0x1.555556p-2f);                      // -1/3
+  p = __builtin_fmaf(ax * x2, p, ax);
+  return __builtin_copysignf(ax < 0.125f ? p : big, x);
+}
+
 // sin / cos: Cody-Waite reduction by pi/2 with a three-part constant (P1 + P2 + P3 = pi/2 to ~2^-75;
 // the first FMA is exact for the quadrants below 2^17), then Taylor polynomials for sin and cos on
 // [-pi/4, pi/4] (truncation below 2^-28). Arguments of magnitude 2^17 and beyond take the library's

@@ -267,7 +267,7 @@ std::string KernelWriter::value(uint32_t vid, const std::vector<std::string>& co
           case Unary::exp: e = (f ? "accy::exp_f32(" : "exp(") + x + ")"; break;
           case Unary::log: e = (f ? "logf(" : "log(") + x + ")"; break;
           case Unary::sqrt: e = (f ? "sqrtf(" : "sqrt(") + x + ")"; break;
-          case Unary::tanh: e = (f ? "tanhf(" : "tanh(") + x + ")"; break;
+          case Unary::tanh: e = (f ? "accy::tanh_f32(" : "tanh(") + x + ")"; break;
           case Unary::sin: e = (f ? "accy::sin_f32(" : "sin(") + x + ")"; break;
           case Unary::cos: e = (f ? "accy::cos_f32(" : "cos(") + x + ")"; break;
           case Unary::tan: e = (f ? "tanf(" : "tan(") + x + ")"; break;

@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <memory>
 #include <set>
 #include <sstream>
 
@@ -1150,36 +1151,124 @@ class Planner {
     gemm(v, gs, os);
   }
 
-  // Writes the contraction described by gs into the slot of value v (laid out per os).
+  // ---- contraction epilogues ----
+  //
+  // When the contraction's value v is not itself materialised and every use of it runs through
+  // elementwise operations of v's shape into exactly one materialised value u (an activation, a
+  // residual add), the kernel's epilogue computes u from the accumulator and stores u: v never
+  // travels through HBM. Other operands of u's expression are read at the same index.
+  bool epilogue_target(uint32_t v, uint32_t& target) const {
+    if (needed_[v] || slots_.slot_of[v] >= 0) return false;
+    const Type& vt = g_.type(v);
+    std::vector<std::vector<uint32_t>> users(g_.ops.size());
+    for (uint32_t u = v + 1; u < g_.ops.size(); ++u)
+      if (live_[u] && !done_[u])
+        for (uint32_t a : g_.ops[u].args) users[a].push_back(u);
+    std::set<uint32_t> region = {v}, targets;
+    std::vector<uint32_t> stack = {v};
+    while (!stack.empty()) {
+      uint32_t x = stack.back();
+      stack.pop_back();
+      for (uint32_t u : users[x]) {
+        const Op& uo = g_.ops[u];
+        bool elementwise = uo.kind == Kind::unary || uo.kind == Kind::binary || uo.kind == Kind::select ||
+                           uo.kind == Kind::compare;
+        if (!elementwise || !(uo.result.dims == vt.dims)) return false;
+        if (needed_[u]) {
+          targets.insert(u);
+        } else if (!region.count(u)) {
+          region.insert(u);
+          stack.push_back(u);
+        }
+      }
+    }
+    if (targets.size() != 1) return false;
+    target = *targets.begin();
+    return !done_[target];
+  }
+
+  // Writes the contraction described by gs into the slot of value v (laid out per os), or, with a
+  // fused epilogue, the value that the elementwise region after v materialises.
   void gemm(uint32_t v, const GemmShape& gs, const OutStrides& os) {
     const Op& op = g_.ops[v];
-    int out = slots_.slot_of[v] >= 0 ? slots_.slot_of[v] : temp_slot(v);
     DType d = op.result.dtype;
-    KernelWriter w(g_, slots_, "i64_t");
-    std::string a = w.arg(gs.a.slot, false), b = w.arg(gs.b.slot, false), c = w.arg(out, true);
-    std::string nm = name("gemm", v);
-    std::ostringstream src;
-    KernelStep k;
-    // One parameter per distinct buffer (both operands may be the same buffer).
-    const char* et = d == DType::f32 ? "float" : "u16_t";
-    std::string params = std::string("const ") + et + "* __restrict__ " + a;
-    if (b != a) params += std::string(", const ") + et + "* __restrict__ " + b;
-    params += std::string(", ") + et + "* __restrict__ " + c;
     const std::string cidx = "b * " + std::to_string(os.b) + "L + m * " + std::to_string(os.m) + "L + n * " +
                              std::to_string(os.n) + "L";
+    std::string nm = name("gemm", v);
+    uint32_t target = v;
+    std::unique_ptr<KernelWriter> w;
+    std::ostringstream epi;
+    // The fused epilogue (dot_general results only: os is their row-major layout).
+    const bool rowmajor = os.b == gs.m * gs.n && os.m == gs.n && os.n == 1;
+    if (op.kind == Kind::dot_general && rowmajor && epilogue_target(v, target)) {
+      try {
+        w.reset(new KernelWriter(g_, slots_, "i64_t"));
+        w->arg(gs.a.slot, false);
+        w->arg(gs.b.slot, false);
+        const Type& rt = op.result;
+        const size_t nb = op.lhs_batch.size();
+        const size_t nlf = rt.rank() - nb - (g_.type(op.args[1]).rank() - op.rhs_batch.size() - op.rhs_contract.size());
+        std::vector<Dim> bd(rt.dims.begin(), rt.dims.begin() + (long)nb);
+        std::vector<Dim> md(rt.dims.begin() + (long)nb, rt.dims.begin() + (long)(nb + nlf));
+        std::vector<Dim> ndims(rt.dims.begin() + (long)(nb + nlf), rt.dims.end());
+        std::vector<std::string> coords;
+        for (auto& c : delinearize("b", bd)) coords.push_back(c);
+        for (auto& c : delinearize("m", md)) coords.push_back(c);
+        for (auto& c : delinearize("n", ndims)) coords.push_back(c);
+        Scope sc(epi, "    ");
+        w->provide = [&](uint32_t vid, const std::vector<std::string>& c, std::string& out) -> bool {
+          if (vid != v) return false;
+          if (c != coords) throw NotFusable("contraction value read at another index");
+          out = "vv";
+          return true;
+        };
+        std::string x = w->value(target, coords, sc);
+        int out = slots_.slot_of[target] >= 0 ? slots_.slot_of[target] : temp_slot(target);
+        epi << sc.indent << w->store(out, cidx, g_.type(target).dtype, x) << "\n";
+      } catch (const NotFusable&) {
+        target = v;
+        w.reset();
+        epi.str("");
+      }
+    }
+    if (!w) {
+      w.reset(new KernelWriter(g_, slots_, "i64_t"));
+      w->arg(gs.a.slot, false);
+      w->arg(gs.b.slot, false);
+      int out = slots_.slot_of[v] >= 0 ? slots_.slot_of[v] : temp_slot(v);
+      epi << "    " << w->store(out, cidx, d, "v") << "\n";
+    }
+    const std::string a = w->arg(gs.a.slot, false), b = w->arg(gs.b.slot, false);
+    // Epilogue functor: every buffer of the kernel as a member named like the kernel parameter.
+    std::ostringstream members, inits;
+    {
+      std::string pl = w->params();
+      size_t start = 0;
+      while (start < pl.size()) {
+        size_t comma = pl.find(", ", start);
+        std::string decl = pl.substr(start, comma == std::string::npos ? std::string::npos : comma - start);
+        members << "  " << decl << ";\n";
+        size_t sp = decl.rfind(' ');
+        inits << (inits.tellp() > 0 ? ", " : "") << decl.substr(sp + 1);
+        if (comma == std::string::npos) break;
+        start = comma + 2;
+      }
+    }
+    std::ostringstream src;
+    KernelStep k;
+    src << "#include \"gemm\"\n";
+    src << "struct Epi_" << nm << " {\n" << members.str()
+        << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
+        << (target != v ? "    const float vv = " + round_to(d, "v") + ";\n" : "") << epi.str() << "  }\n};\n";
     if (d == DType::f32) {
       // f32 on v_mfma_f32_32x32x2_f32: exact 256 x 256 x 32 tiles (gemm_eligible checked the layout).
-      src << "#include \"gemm\"\n";
       src << "struct Cfg_" << nm << " {\n"
           << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
           << gs.ga_b.fn("a_b") << gs.ga_m.fn("a_m") << gs.ga_k.fn("a_k") << gs.gb_b.fn("b_b") << gs.gb_k.fn("b_k")
           << gs.gb_n.fn("b_n") << "};\n";
-      src << "struct Epi_" << nm << " {\n  float* __restrict__ c;\n"
-          << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const { c[" << cidx
-          << "] = v; }\n};\n";
-      src << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << params << ") {\n"
+      src << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << w->params() << ") {\n"
           << "  accy::gemm::mma32f<Cfg_" << nm << ">(" << a << " + " << gs.a.offset << "L, " << b << " + "
-          << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
+          << gs.b.offset << "L, Epi_" << nm << "{" << inits.str() << "});\n}\n";
       k.grid[0] = (uint32_t)((gs.m / 256) * (gs.n / 256));
       k.block[0] = 256;
     } else {
@@ -1188,10 +1277,10 @@ class Planner {
       const int BM = 256, BN = 256, BK = 64;
       int WM = 2, WN = 2;
       if (const char* e = std::getenv("ACCY_GEMM_WAVES")) {
-        int m = 0, n = 0;
-        if (std::sscanf(e, "%dx%d", &m, &n) == 2 && (m == 2 || m == 4) && (n == 2 || n == 4) && m * n <= 8) {
-          WM = m;
-          WN = n;
+        int mm = 0, nn = 0;
+        if (std::sscanf(e, "%dx%d", &mm, &nn) == 2 && (mm == 2 || mm == 4) && (nn == 2 || nn == 4) && mm * nn <= 8) {
+          WM = mm;
+          WN = nn;
         }
       }
       // Direct-to-LDS pipeline when the tiles divide the problem exactly (every row start 16-byte
@@ -1199,7 +1288,6 @@ class Planner {
       int dm = 0, dn = 0;
       bool akc = gs.a_k == 1, bkc = gs.b_k == 1;
       bool dma = dma_eligible(gs, dm, dn, akc, bkc);
-      src << "#include \"gemm\"\n";
       src << "struct Cfg_" << nm << " {\n"
           << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
           << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
@@ -1215,13 +1303,10 @@ class Planner {
         src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
             << ", WAVES_N = " << WN << ";\n};\n";
       }
-      src << "struct Epi_" << nm << " {\n  u16_t* __restrict__ c;\n"
-          << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
-          << "    c[" << cidx << "] = accy::f32_to_" << (d == DType::bf16 ? "bf16" : "f16") << "(v);\n  }\n};\n";
       int threads = dma ? 256 : WM * WN * 64;
-      src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(" << params << ") {\n"
+      src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(" << w->params() << ") {\n"
           << "  accy::gemm::" << (dma ? "mma16_dma" : "mma16") << "<Cfg_" << nm << ">(" << a << " + " << gs.a.offset
-          << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << c << "});\n}\n";
+          << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << inits.str() << "});\n}\n";
       int64_t tiles = dma ? (gs.m / dm) * (gs.n / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
       k.grid[0] = (uint32_t)tiles;
       k.block[0] = threads;
@@ -1231,10 +1316,15 @@ class Planner {
     k.name = nm;
     k.grid[1] = (uint32_t)gs.batch;
     k.klass = "gemm";
-    k.label = "gemm:%" + std::to_string(v);
+    k.label = "gemm:%" + std::to_string(v) + (target != v ? "+%" + std::to_string(target) : "");
     k.algorithmic_flops = 2.0 * (double)gs.batch * (double)gs.m * (double)gs.n * (double)gs.k;
-    push(std::move(k), w);
-    finish(v);
+    push(std::move(k), *w);
+    if (target != v) {
+      done_[v] = true;
+      finish(target);
+    } else {
+      finish(v);
+    }
   }
 
   // ---- sum over k of mul(A, B): the same contraction, spelled elementwise ----

@@ -363,6 +363,26 @@ def test_gemm_bf16_full_size_on_sampled_rows():
     assert_normwise(got[rows], ref, 2e-2, "bf16")
 
 
+# ---- device math against the mathematics ----
+
+def test_device_tanh_against_float64():
+    """accy::tanh_f32 (exp2 / reciprocal form above |x| = 1/8, odd polynomial below) within 2e-6
+    relative of float64 tanh, with tanh(+-inf) = +-1, NaN propagated and tanh(-0) = -0."""
+    x = np.concatenate([np.linspace(-12, 12, 24001), np.geomspace(1e-30, 1, 3000), -np.geomspace(1e-30, 1, 3000),
+                        [0.125, np.nextafter(np.float32(0.125), np.float32(0)), -0.125, 88.0, -88.0, 1e-40]])
+    x = x.astype(np.float32)
+    special = np.array([np.inf, -np.inf, np.nan, -0.0, 0.0], np.float32)
+    xs = np.concatenate([x, special])
+    prog = T.define("tanh", [T.spec("f32", i=len(xs))], lambda b, a: a[0].tanh())
+    got = hip_run(prog, [xs])[0]
+    ref = np.tanh(x.astype(np.float64))
+    err = np.abs(got[:len(x)].astype(np.float64) - ref)
+    assert (err <= 2e-6 * np.abs(ref) + 1e-37).all(), f"worst {(err / np.maximum(np.abs(ref), 1e-37)).max():.3e}"
+    tail = got[len(x):]
+    assert tail[0] == 1.0 and tail[1] == -1.0 and np.isnan(tail[2])
+    assert tail[3] == 0.0 and np.signbit(tail[3]) and tail[4] == 0.0 and not np.signbit(tail[4])
+
+
 # ---- exact classes ----
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])

@@ -288,6 +288,8 @@ int accy_hip_kernel_info(accy_hip_handle h, size_t index, accy_hip_kernel_stats*
   out->algorithmic_bytes = t[index].algorithmic_bytes;
   out->algorithmic_flops = t[index].algorithmic_flops;
   out->last_ms = t[index].last_ms;
+  out->mean_ms = t[index].mean_ms;
+  out->calls = t[index].calls;
   return ACCY_HIP_OK;
 }
 

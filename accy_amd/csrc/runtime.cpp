@@ -5,6 +5,7 @@
 
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <unordered_map>
@@ -160,19 +161,49 @@ Executor::~Executor() {
 }
 
 void Executor::set_profiling(bool on) {
-  profiling_ = on;
-  if (on && events_.empty()) {
-    size_t n = 0;
-    for (const Step& st : plan_.steps)
-      if (st.type == Step::Kernel) ++n;
-    events_.resize(2 * n);
-    for (auto& e : events_) check(hipEventCreate(&e), "hipEventCreate");
+  if (on) {
+    recorded_ = 0;
+    pending_ = false;
   }
+  profiling_ = on;
+}
+
+const std::vector<KernelTiming>& Executor::timings() {
+  if (!pending_) return timings_;
+  const size_t nk = timings_.size(), n = std::min(recorded_, kProfiledCalls);
+  const size_t last = (recorded_ - 1) % kProfiledCalls;
+  // Each invocation's events are in stream order: its last end event completes after the others.
+  for (size_t c = 0; c < n; ++c) check(hipEventSynchronize(events_[(c * nk + nk - 1) * 2 + 1]), "hipEventSynchronize");
+  for (size_t k = 0; k < nk; ++k) {
+    double sum = 0;
+    for (size_t c = 0; c < n; ++c) {
+      float ms = 0;
+      check(hipEventElapsedTime(&ms, events_[(c * nk + k) * 2], events_[(c * nk + k) * 2 + 1]), "hipEventElapsedTime");
+      sum += ms;
+      if (c == last) timings_[k].last_ms = ms;
+    }
+    timings_[k].mean_ms = n ? (float)(sum / (double)n) : 0.0f;
+    timings_[k].calls = (uint32_t)n;
+  }
+  pending_ = false;
+  return timings_;
 }
 
 void Executor::run_steps(hipStream_t stream) {
   for (size_t i = 0; i < plan_.slots.size(); ++i)
     if (plan_.slots[i].role == SlotInfo::Temp || plan_.slots[i].role == SlotInfo::Const) bound_[i] = owned_[i];
+  // Event slot of this invocation when profiling (created on first use).
+  const size_t nk = timings_.size();
+  hipEvent_t* ev = nullptr;
+  if (profiling_ && nk) {
+    const size_t slot = recorded_ % kProfiledCalls;
+    if (events_.size() < (slot + 1) * nk * 2) {
+      size_t old = events_.size();
+      events_.resize((slot + 1) * nk * 2, nullptr);
+      for (size_t e = old; e < events_.size(); ++e) check(hipEventCreate(&events_[e]), "hipEventCreate");
+    }
+    ev = &events_[slot * nk * 2];
+  }
   size_t ki = 0;
   for (size_t i = 0; i < plan_.steps.size(); ++i) {
     const Step& st = plan_.steps[i];
@@ -189,12 +220,16 @@ void Executor::run_steps(hipStream_t stream) {
       ptrs[a] = bound_[(size_t)k.args[a]];
       params[a] = &ptrs[a];
     }
-    if (profiling_) check(hipEventRecord(events_[2 * ki], stream), "hipEventRecord");
+    if (ev) check(hipEventRecord(ev[2 * ki], stream), "hipEventRecord");
     check(hipModuleLaunchKernel(fn_[i], k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2],
                                 k.shared_bytes, stream, params.data(), nullptr),
           "hipModuleLaunchKernel");
-    if (profiling_) check(hipEventRecord(events_[2 * ki + 1], stream), "hipEventRecord");
+    if (ev) check(hipEventRecord(ev[2 * ki + 1], stream), "hipEventRecord");
     ++ki;
+  }
+  if (ev) {
+    ++recorded_;
+    pending_ = true;
   }
 }
 
@@ -205,11 +240,6 @@ void Executor::invoke_device(const void* const* inputs, size_t n_inputs, void* c
   for (size_t i = 0; i < n_inputs; ++i) bound_[(size_t)plan_.input_slots[i]] = const_cast<void*>(inputs[i]);
   for (size_t i = 0; i < n_outputs; ++i) bound_[(size_t)plan_.output_slots[i]] = outputs[i];
   run_steps(stream);
-  if (profiling_) {
-    check(hipStreamSynchronize(stream), "hipStreamSynchronize");
-    for (size_t k = 0; k < timings_.size(); ++k)
-      check(hipEventElapsedTime(&timings_[k].last_ms, events_[2 * k], events_[2 * k + 1]), "hipEventElapsedTime");
-  }
 }
 
 void Executor::invoke_host(const void* const* inputs, const size_t* input_lens, size_t n_inputs,

@@ -34,7 +34,9 @@ std::string full_kernel_source(const std::string& body);
 struct KernelTiming {
   std::string label, klass;
   double algorithmic_bytes = 0, algorithmic_flops = 0;
-  float last_ms = 0;
+  float last_ms = 0;   // the latest recorded invocation
+  float mean_ms = 0;   // mean over the recorded invocations
+  uint32_t calls = 0;  // recorded invocations (at most kProfiledCalls)
 };
 
 // A compiled program bound to device memory: the HIP counterpart of the reference's loaded fragment.
@@ -55,8 +57,13 @@ class Executor {
   void invoke_device(const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs,
                      hipStream_t stream);
 
+  // While profiling is on, every invocation records a HIP event pair around each kernel on the
+  // launch stream (no synchronisation, so back-to-back invocations keep their steady state);
+  // timings() waits for the recorded work and reports the last and the mean duration. Turning
+  // profiling on starts a new measurement.
+  static constexpr size_t kProfiledCalls = 256;
   void set_profiling(bool on);
-  const std::vector<KernelTiming>& timings() const { return timings_; }
+  const std::vector<KernelTiming>& timings();
 
  private:
   void run_steps(hipStream_t stream);
@@ -67,7 +74,9 @@ class Executor {
   std::vector<hipFunction_t> fn_;
   hipStream_t stream_ = nullptr;
   bool profiling_ = false;
-  std::vector<hipEvent_t> events_;
+  bool pending_ = false;           // recorded events not yet read back
+  size_t recorded_ = 0;            // invocations recorded since profiling was turned on
+  std::vector<hipEvent_t> events_;  // kProfiledCalls slots of 2 events per kernel
   std::vector<KernelTiming> timings_;
 };
 

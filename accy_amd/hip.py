@@ -59,7 +59,8 @@ class _Descriptor(ctypes.Structure):
 
 class _KernelStats(ctypes.Structure):
     _fields_ = [("label", ctypes.c_char_p), ("klass", ctypes.c_char_p), ("algorithmic_bytes", ctypes.c_double),
-                ("algorithmic_flops", ctypes.c_double), ("last_ms", ctypes.c_float)]
+                ("algorithmic_flops", ctypes.c_double), ("last_ms", ctypes.c_float), ("mean_ms", ctypes.c_float),
+                ("calls", ctypes.c_uint32)]
 
 
 @dataclass(frozen=True)
@@ -73,11 +74,15 @@ class Descriptor:
 
 @dataclass
 class KernelStats:
+    """One kernel: algorithmic work, and (while profiling) the latest and the mean duration over the
+    recorded invocations."""
     label: str
     klass: str
     algorithmic_bytes: float
     algorithmic_flops: float
     last_ms: float
+    mean_ms: float = 0.0
+    calls: int = 0
 
 
 _lib = None
@@ -247,7 +252,7 @@ class Session:
             k = _KernelStats()
             _check(self._lib.accy_hip_kernel_info(h, i, ctypes.byref(k)))
             out.append(KernelStats(k.label.decode(), k.klass.decode(), k.algorithmic_bytes, k.algorithmic_flops,
-                                   k.last_ms))
+                                   k.last_ms, k.mean_ms, k.calls))
         return out
 
 

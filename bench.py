@@ -8,7 +8,10 @@
   algorithmic FLOP (MFMA / VALU-bound configs) per second, with the per-config figures of the
   measurement plan.
 * ``roofline`` is for the dominant kernel: its algorithmic bytes or FLOP per launch divided by its
-  average duration, measured with HIP events recorded on the launch stream around that kernel.
+  average duration, from HIP events on the launch stream: around the timed region for a one-kernel
+  program, around that kernel in each of K back-to-back steps otherwise. ``traffic`` is the HBM
+  bytes per launch measured with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, calibrated on a copy
+  kernel) and committed in profiles/traffic.json; null for a workload not measured there.
 * ``cpu_baseline`` is the CPU oracle (the runCpu restatement, oracle/) timed on this host on a
   bounded sample of the same workload, then scaled to the metric's unit (kind "port").
 
@@ -39,6 +42,19 @@ METRIC = "GB/s & TFLOP/s per config as % of MI355X roofline; speedup vs runCpu"
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0, "f16": 2500.0}
 VALU_PEAK_TFLOPS = 157.3
+
+
+TRAFFIC = Path(__file__).resolve().parent / "profiles" / "traffic.json"
+
+
+def measured_traffic(config: str, label: str):
+    """HBM bytes per launch of one kernel from the committed rocprofv3 counter measurement
+    (FETCH_SIZE and WRITE_SIZE, calibrated on a copy kernel), or None when not measured."""
+    try:
+        table = json.loads(TRAFFIC.read_text()).get(config, {})
+    except (OSError, ValueError):
+        return None
+    return table.get(label, table.get(label.split("+")[0]))
 
 
 def decoder_flops(batch, seq, model, heads, hd, ffn):
@@ -165,20 +181,21 @@ def main() -> int:
     end.record(stream)
     stream.synchronize()
     elapsed = time.perf_counter() - t0
-    ms_per_step = max(elapsed * 1e3, start.elapsed_ms(end)) / args.steps
+    event_ms = start.elapsed_ms(end) / args.steps
+    ms_per_step = max(elapsed * 1e3 / args.steps, event_ms)
 
-    # Per-kernel durations: HIP events recorded on the launch stream around each kernel.
+    # Per-kernel durations: HIP events recorded on the launch stream around each kernel, over the
+    # same number of back-to-back steps (no synchronisation between them).
     ex.set_profiling(True)
-    per_kernel = {}
-    reps = max(3, min(args.steps, 10))
-    for _ in range(reps):
+    for _ in range(args.steps):
         step()
-        for k in ex.kernels():
-            per_kernel.setdefault(k.label, []).append((k.last_ms, k))
+    per_kernel = {k.label: k for k in ex.kernels()}
     ex.set_profiling(False)
-    dominant = max(per_kernel.items(), key=lambda kv: sum(m for m, _ in kv[1]))
-    dom_ms = float(np.mean([m for m, _ in dominant[1]]))
-    dom_stats = dominant[1][0][1]
+    dominant = max(per_kernel.items(), key=lambda kv: kv[1].mean_ms)
+    dom_stats = dominant[1]
+    # A one-kernel program's kernel duration is the events around the timed region over the steps
+    # (events around each launch add a few microseconds each); several kernels need their own events.
+    dom_ms = event_ms if len(per_kernel) == 1 else float(dom_stats.mean_ms)
     scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
     value = cfg["work"] / (ms_per_step * 1e-3) / scale
     # The roofline is the dominant kernel's: a one-kernel program's work is the config's; in a
@@ -188,13 +205,13 @@ def main() -> int:
         work = cfg["work"] if single else dom_stats.algorithmic_bytes
         achieved = work / (dom_ms * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=achieved, peak=cfg["peak"], unit="GB/s", frac=achieved / cfg["peak"],
-                    traffic=None, kernel=dominant[0], kernel_ms=dom_ms)
+                    traffic=measured_traffic(args.config, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
     else:
         work = cfg["work"] if single else dom_stats.algorithmic_flops
         achieved = work / (dom_ms * 1e-3) / 1e12
         peak = cfg["peak"] / 1000.0 if cfg["unit"] == "GFLOP/s" else cfg["peak"]
         roof = dict(bound=cfg["bound"], achieved=achieved, peak=peak, unit="TFLOP/s", frac=achieved / peak,
-                    traffic=None, kernel=dominant[0], kernel_ms=dom_ms)
+                    traffic=measured_traffic(args.config, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
     cpu = None if args.no_cpu else oracle_time(cfg)
     line = {
         "metric": METRIC, "value": value, "unit": cfg["unit"], "n_gpus": 1, "steps": args.steps,
@@ -202,7 +219,7 @@ def main() -> int:
         "vs_baseline": None, "dtype": cfg["dtype"], "data": "synthetic (seeded SplitMix64)",
         "config": dict(workload=args.config, **cfg["workload"]),
         "roofline": roof, "cpu_baseline": cpu,
-        "kernels": {lbl: float(np.mean([m for m, _ in v])) for lbl, v in per_kernel.items()},
+        "kernels": {lbl: float(k.mean_ms) for lbl, k in per_kernel.items()},
     }
     ex.deinit()
     for b in dins + douts:

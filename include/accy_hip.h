@@ -55,13 +55,18 @@ typedef struct {
   uint32_t alignment;
 } accy_hip_descriptor;
 
-/* One kernel of a compiled program, for measurement. `last_ms` is filled when profiling is on. */
+/* One kernel of a compiled program, for measurement. While profiling is on, every invocation
+ * records HIP events around each kernel on its launch stream without synchronising; reading the
+ * stats waits for them. `last_ms` is the latest invocation, `mean_ms` the mean over the `calls`
+ * invocations recorded since profiling was turned on (the latest 256). */
 typedef struct {
   const char* label;
   const char* klass;
   double algorithmic_bytes;
   double algorithmic_flops;
   float last_ms;
+  float mean_ms;
+  uint32_t calls;
 } accy_hip_kernel_stats;
 
 /* One-shot run: compile, copy inputs in, launch, copy outputs out, release.

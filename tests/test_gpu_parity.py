@@ -486,7 +486,20 @@ def test_executor_launches_many_times_and_device_invoke():
         ex.set_profiling(True)
         ex.launch_device([dx.ptr], [dout.ptr], stream.handle)
         ks = ex.kernels()
-        assert len(ks) == 1 and ks[0].klass == "row" and ks[0].last_ms > 0
+        assert len(ks) == 1 and ks[0].klass == "row" and ks[0].last_ms > 0 and ks[0].calls == 1
+        # back-to-back invocations are recorded without synchronisation and averaged on read;
+        # turning profiling on again starts a new measurement; the latest 256 are kept
+        for _ in range(5):
+            ex.launch_device([dx.ptr], [dout.ptr], stream.handle)
+        ks = ex.kernels()
+        assert ks[0].calls == 6 and ks[0].mean_ms > 0
+        ex.set_profiling(True)
+        for _ in range(300):
+            ex.launch_device([dx.ptr], [dout.ptr], stream.handle)
+        ks = ex.kernels()
+        assert ks[0].calls == 256 and ks[0].mean_ms > 0
+        ex.set_profiling(False)
+        assert_rel(dout.download(np.zeros(64, np.float32)), ref, 1e-5)
         for b in (dx, dout):
             b.free()
         stream.destroy()

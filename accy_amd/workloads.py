@@ -101,6 +101,24 @@ def tone_program(guesses: int = 8192, points: int = 16384, scalar: bool = False)
     return T.define("mismatch", [freq, T.spec("f32", point=points), T.spec("f32", point=points)], mismatch)
 
 
+def mismatch_and_slope(b: T.Builder, args: List[T.Value]) -> List[T.Value]:
+    """The README's `valueAndGrad(.wrt = frequency)` of the mismatch, vmapped over guesses
+    (examples/consumer/src/main.zig:80-102; README.md:290-304): the mismatch and its derivative
+    sum(2 (sin(f t) - s) cos(f t) t), written out as the two reductions the derivative program
+    computes (the reference's autodiff is not available here, so its exact op order is not)."""
+    frequency, time, sample = args
+    phase = frequency.mul(time)
+    difference = phase.sin().sub(sample)
+    value = difference.mul(difference).sum("point")
+    slope = difference.mul(b.full_float(T.Type("f32", ()), 2.0)).mul(phase.cos()).mul(time).sum("point")
+    return [value, slope]
+
+
+def tone_value_and_slope_program(guesses: int = 8, points: int = 16) -> T.Program:
+    specs = [T.spec("f32", guess=guesses), T.spec("f32", point=points), T.spec("f32", point=points)]
+    return T.define("mismatch_and_slope", specs, mismatch_and_slope)
+
+
 def tone_inputs(guesses: int = 8192, points: int = 16384, seed: int = 1) -> List[np.ndarray]:
     frequency = uniform(seed, guesses, 0.5, 5.0).astype(np.float32)
     time = (np.arange(points, dtype=np.float32) * np.float32(0.25)).astype(np.float32)

@@ -57,6 +57,20 @@ def measured_traffic(config: str, label: str):
     return table.get(label, table.get(label.split("+")[0]))
 
 
+VALU = Path(__file__).resolve().parent / "profiles" / "valu.json"
+VALU_ISSUE_PEAK = 256 * 2.4e9  # wave64 VALU instructions per second: one per CU per clock
+
+
+def measured_valu(config: str, label: str):
+    """VALU instructions (wave64) per launch of one kernel from the committed rocprofv3
+    SQ_INSTS_VALU measurement, or None."""
+    try:
+        table = json.loads(VALU.read_text()).get(config, {})
+    except (OSError, ValueError):
+        return None
+    return table.get(label, table.get(label.split("+")[0]))
+
+
 def decoder_flops(batch, seq, model, heads, hd, ffn):
     """Useful flops of one decoder block: the four projections, the two MLP contractions, and causal
     attention over the key <= query pairs (scores and P.V, 2 flops per multiply-add each)."""
@@ -120,27 +134,37 @@ def config_table():
     }
 
 
-def oracle_time(cfg, budget_s: float = 10.0):
-    """Times the CPU oracle on the config's bounded sample; repeats until `budget_s` is spent."""
+def oracle_time(cfg, budget_s: float = 8.0):
+    """Times the CPU oracle on the config's bounded sample, with all host threads (capped at 16) and
+    with one thread (runCpu launches single-threaded); each until `budget_s` is spent (at most 10
+    runs). The oracle's per-output order makes both bit-identical."""
     sys.path.insert(0, str(ROOT / "tests"))
     from conftest import oracle_lib, oracle_run
     prog, ins, work = cfg["sample"]()
     lib = oracle_lib()
     threads = int(os.environ.get("ACCY_CPU_THREADS", "0")) or (os.cpu_count() or 1)
     threads = min(threads, 16)
-    lib.accy_cpu_set_threads(threads)
-    times = []
-    start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        oracle_run(prog, ins)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - start >= budget_s or len(times) >= 20:
-            break
-    t = float(np.median(times))
     scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
-    return dict(value=work / t / scale, unit=cfg["unit"], cores=threads, kind="port",
-                sample=f"{cfg['sample_desc']}; median of {len(times)} runs, {t:.3f} s each")
+
+    def timed(n):
+        lib.accy_cpu_set_threads(n)
+        times = []
+        start = time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            oracle_run(prog, ins)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - start >= budget_s or len(times) >= 10:
+                break
+        return float(np.median(times)), len(times)
+
+    t_all, n_all = timed(threads)
+    t_one, n_one = timed(1)
+    lib.accy_cpu_set_threads(threads)
+    return dict(value=work / t_all / scale, unit=cfg["unit"], cores=threads, kind="port",
+                sample=f"{cfg['sample_desc']}; median of {n_all} runs, {t_all:.3f} s each",
+                single_core=dict(value=work / t_one / scale, cores=1,
+                                 sample=f"median of {n_one} runs, {t_one:.3f} s each"))
 
 
 def main() -> int:
@@ -212,6 +236,10 @@ def main() -> int:
         peak = cfg["peak"] / 1000.0 if cfg["unit"] == "GFLOP/s" else cfg["peak"]
         roof = dict(bound=cfg["bound"], achieved=achieved, peak=peak, unit="TFLOP/s", frac=achieved / peak,
                     traffic=measured_traffic(args.config, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
+    insts = measured_valu(args.config, dominant[0])
+    if insts is not None:
+        # VALU issue fraction (instructions x 64 lanes per second against 256 CUs x 2.4 GHz x 64)
+        roof["valu_issue"] = dict(insts_per_launch=insts, frac=insts / (dom_ms * 1e-3) / VALU_ISSUE_PEAK)
     cpu = None if args.no_cpu else oracle_time(cfg)
     line = {
         "metric": METRIC, "value": value, "unit": cfg["unit"], "n_gpus": 1, "steps": args.steps,

@@ -39,6 +39,43 @@ def test_readme_tone_known_answers_on_gpu():
     assert_rel(eight, ref, 1e-5)
 
 
+def test_readme_gradient_descent_on_gpu():
+    """README.md:294-304: the vmapped value-and-slope program; at 2.5 the slope is about -31.29, and
+    100 steps of f -= 0.005 slope from 0.5 .. 7.5 take the guesses that began at 2.5 and 3.5 to about
+    3 with mismatch near zero, the other six to mismatches between 7.9 and 14.6. At the C1 size both
+    reductions share one fused row kernel."""
+    big = W.tone_value_and_slope_program(8192, 16384)
+    assert hip.plan_source(big.encode(), compile=False).count("__global__") == 1
+    time, sample = W.readme_tone()
+    prog = W.tone_value_and_slope_program(8, 16)
+    f = np.array([0.5, 1.5, 2.5, 3.5, 4.5, 5.5, 6.5, 7.5], np.float32)
+    value, slope = hip_run(prog, [f, time, sample])
+    ref_v, ref_s = oracle_run(prog, [f, time, sample])
+    assert_rel(value, ref_v, 1e-5)
+    assert_rel(slope, ref_s, 1e-5)
+    assert abs(float(slope[2]) - (-31.29)) < 5e-3
+    with hip.Hip(prog) as ex:
+        for _ in range(100):
+            value, slope = np.zeros(8, np.float32), np.zeros(8, np.float32)
+            ex.launch([f, time, sample], [value, slope])
+            f = (f - np.float32(0.005) * slope).astype(np.float32)
+        ex.launch([f, time, sample], [value, slope])
+    assert np.all(np.abs(f[[2, 3]] - 3.0) < 1e-3) and np.all(value[[2, 3]] < 1e-5)
+    others = value[[0, 1, 4, 5, 6, 7]]
+    assert np.all((others > 7.9) & (others < 14.6)), others
+    say("value and slope 8192 x 16384 (full C1 size, one row kernel)")
+    ins = W.tone_inputs(8192, 16384, seed=1)
+    v, s = hip_run(big, ins)
+    idx = np.sort(np.random.default_rng(3).choice(8192, 64, replace=False))
+    rv, rs = oracle_run(W.tone_value_and_slope_program(64, 16384), [ins[0][idx], ins[1], ins[2]])
+    assert_rel(v[idx], rv, 1e-5)
+    # the slope is a sum of terms of both signs: relative to the sum of their magnitudes
+    scale = oracle_run(T.define("mag", [T.spec("f32", guess=64), T.spec("f32", point=16384), T.spec("f32", point=16384)],
+                                lambda b, a: a[0].mul(a[1]).sin().sub(a[2]).abs().mul(a[1]).sum("point")),
+                       [ins[0][idx], ins[1], ins[2]])[0]
+    assert np.all(np.abs(s[idx].astype(np.float64) - rs) <= 2e-5 * 2 * scale), np.abs(s[idx] - rs) / scale
+
+
 # ---- C1 tone and C2 logsumexp ----
 
 def test_tone_subset_matches_oracle():

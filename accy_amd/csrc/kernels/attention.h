@@ -1,35 +1,38 @@
 // Fused attention O[b, q, :] = softmax_k(scale * Q[b, q, :] . K[b, k, :] [masked k > q]) V[b, k, :] on
 // gfx950 matrix cores, for 16-bit Q, K, V with a head dimension of 128 (both for Q.K and for V).
 //
-// One workgroup of WAVES wavefronts owns 64 * WAVES queries of one batch index and streams the keys
-// in blocks of 64. Each wave owns two 32-query tiles (queries q0 + 32 w and q0 + 32 (WAVES + w), so
-// that under a causal mask every wave of the group has almost the same work).
+// A workgroup of 2 * WAVES wavefronts owns 64 * WAVES queries of one batch index and streams the
+// keys in blocks of 32. Each group of 64 queries (two 32-query tiles, q0 + 32 w and
+// q0 + 32 (WAVES + w), so that under a causal mask every group has almost the same work) is served
+// by a scorer wave (S and softmax) and an accumulator wave (P.V and the output); see the work split
+// below.
 //
 // Orientation: the scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16. In the
 // 32 x 32 accumulator layout lane l then holds one query (column l % 32) and 16 keys (rows
 // 8 g + 4 (l / 32) + j at register 4 g + j), so a row maximum or sum over the keys is a register
 // fold plus one exchange with lane l ^ 32. The Q^T operand (B) is the same for every key block and
-// stays in registers. The probabilities P^T are packed to 16 bits in registers and fed back as the B
+// stays in the scorer's registers. The probabilities P^T are packed to 16 bits and serve as the B
 // operand of O^T = V^T P^T: registers 8 s .. 8 s + 7 of a score tile are the B operand of 16-key
 // step s when both operands number the keys of that step in the same permuted order (slot
 // 8 h + 4 r + t holds key 16 s + 8 r + 4 h + t), which the V^T fragment read (ds_read_b64_tr_b16
-// with rows 16 s + 8 r + 4 h + t) follows. No data moves between lanes for the softmax output.
+// with rows 16 s + 8 r + 4 h + t) follows. P crosses from scorer to accumulator through LDS in
+// exactly this register layout (lane-linear 16-byte stores and loads).
 //
 // Softmax: f32 throughout, online over key blocks in the log2 domain: e = exp2(s * scale * log2 e -
 // m) with v_exp_f32. The subtracted maximum m only moves when the running maximum exceeds it by more
 // than 8 (a factor 256), so the accumulators are rescaled rarely; e <= 256 stays well inside the
 // 16-bit range of the P operand. Row sums accumulate the f32 e; the result is O / sum.
 //
-// K and V tiles go straight from global memory to LDS (global_load_lds_dwordx4) three blocks deep,
-// in three distinct LDS arrays per operand so that the compiler's wait analysis can tell the
-// in-flight loads from the reads. Layouts (256-byte rows of 128 elements, conflict-free reads):
+// K and V tiles go straight from global memory to LDS (global_load_lds_dwordx4), four stages per
+// operand in distinct LDS arrays so that the compiler's wait analysis can tell the in-flight loads
+// from the reads. Layouts (256-byte rows of 128 elements, conflict-free reads):
 //  * K: 16-byte chunk c of key row r at chunk c ^ (r & 15); A-operand reads are ds_read_b128.
 //  * V: 32-byte unit u of key row r at unit u ^ (r & 7); A-operand reads are ds_read_b64_tr_b16.
 //
 // The configuration struct C supplies: DT (0 bf16, 1 f16), WAVES, SQ, SK, NB (batch count), the
 // element strides Q_S, K_S, V_S of one query / key row (the head dimension has stride 1), the batch
 // offset functions q_off(b), k_off(b), v_off(b), CAUSAL and SL (the score scale times log2 e, > 0).
-// O is written row-major as [b][q][128].
+// O is written row-major as [b][q][128]. The kernel is launched with 128 * WAVES threads.
 #pragma once
 
 namespace accy {
@@ -39,6 +42,7 @@ using gemm::f32x16;
 using gemm::i16x4;
 using gemm::u32x4;
 typedef u32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Compile-time loop: For<B, E>::run(f) calls f(Int<i>{}) for i = B .. E - 1, so that every register
 // array index in the body is a constant.
@@ -160,39 +164,47 @@ __device__ __forceinline__ float sum_with_partner(float x) {
   return a + b;
 }
 
-// Software pipeline per wave, iteration j (key block j of 32 keys):
-//   A: the 16 MFMAs of S(j) = K(j) Q^T, with the softmax of block j - 1 slotted between them
-//      (slots 0-3 row maxima, slot 4 the exchange with the partner lane and the rare rescale,
-//      slots 5-15 exp2, partial sums and packing of P(j - 1));
-//   B: the 16 MFMAs of O^T += V(j - 1)^T P(j - 1)^T.
-// The softmax VALU work of one block thus issues under the MFMAs of the next. S alternates between
-// two register sets by block parity (no copies); K and V stages are four deep, because V(j - 1) is
-// still read while block j + 2 is loading.
+// Work split. Each group of 64 queries is served by two waves, which the hardware places on one
+// SIMD (waves w and w + WAVES of a workgroup of 2 * WAVES waves):
+//  * the scorer computes S = K Q^T and the softmax and writes P (16-bit, already in the MFMA
+//    B-operand layout) and the rescale factors to LDS;
+//  * the accumulator reads them back and runs O^T += V^T P^T, then normalises and stores O.
+// Each wave then fits in half the register file (the scorer holds Q^T and two score sets, the
+// accumulator O), so the two share a SIMD, and the scorer's softmax VALU work issues while the
+// accumulator's MFMAs run. Step t of the workgroup (one barrier each, nkb + 2 steps):
+//  * scorer: S(t) for t < nkb, with the softmax of block t - 1 slotted between its 16 MFMAs (slots
+//    0-3 row maxima, slot 4 the exchange with the partner lane and the rare rescale, slots 5-15
+//    exp2, partial sums and packing); P(t - 1) and the factors go to buffer (t - 1) % 2;
+//  * accumulator: for t >= 2, block t - 2 from buffer t % 2 and V stage (t - 2) % 4.
+// K tiles are loaded by the scorers two steps ahead (K(t + 2) at step t), V tiles by the
+// accumulators two steps before use (V(t) at step t); both have four LDS stages. A P buffer written
+// at step t is read at step t + 1 and rewritten at step t + 2, after the barrier that follows the
+// reads.
 template <class C>
-struct Flash {
-  static constexpr int WAVES = C::WAVES, BQ = 64 * WAVES, QT = 2, DS = HD / 16, DTN = HD / 32;
-  static constexpr int PER = 2 * (8 / WAVES);  // load instructions per wave per key block
-  static constexpr long NQB = C::SQ / BQ, NKB = C::SK / BK;
-  static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
+struct Lds {
+  static constexpr int WAVES = C::WAVES;
+  u16_t* const* ks;  // K stages [4][BK * HD]
+  u16_t* const* vs;  // V stages [4][BK * HD]
+  u32x4* pb;         // P: [2][WAVES][QT * 2][64] u32x4
+  float* ab;         // rescale factors: [2][WAVES][64][QT]
+  float* lb;         // row sums for the epilogue: [WAVES][64][QT]
+};
 
+template <class C>
+struct Scorer {
+  static constexpr int WAVES = C::WAVES, QT = 2, DS = HD / 16;
+  static constexpr int PER = 8 / WAVES;  // K load instructions per wave per key block
+  static constexpr long NQB = C::SQ / (64 * WAVES), NKB = C::SK / BK;
+
+  Lds<C> sh;
   const u16_t* __restrict__ kb;
-  const u16_t* __restrict__ vb;
-  u16_t* const* ks;
-  u16_t* const* vs;
   u32x4 qf[QT][DS];
-  f32x16 o[QT][DTN];
   f32x16 s[2][QT];  // scores of the blocks of even / odd index
   float m[QT], l[QT];
   long q0;
   int wave, lane;
 
   __device__ __forceinline__ long query(int qt) const { return q0 + 32 * (qt * WAVES + wave) + (lane & 31); }
-
-  template <int ST>
-  __device__ __forceinline__ void issue(long j) {
-    load_k<WAVES, C::K_S>(kb, j * BK, ks[ST], wave, lane);
-    load_v<WAVES, C::V_S>(vb, j * BK, vs[ST], wave, lane);
-  }
 
   // Scores of keys above the query are -inf (blocks that cross the diagonal only).
   template <int PB>
@@ -209,9 +221,11 @@ struct Flash {
     }
   }
 
-  // Softmax work of slot T (see above) on the scores in set PB; p receives P as MFMA B operands.
+  // Softmax work of slot T on the scores in set PB; p receives P as MFMA B operands, alpha the
+  // factor by which the accumulated O is to be scaled before P.V of this block (1 if unchanged).
   template <int PB, int T>
-  __device__ __forceinline__ void softmax_slot(float (&mx)[QT], float (&msub)[QT], float (&ls)[QT][4], u32x4 (&p)[QT][2]) {
+  __device__ __forceinline__ void softmax_slot(float (&mx)[QT], float (&msub)[QT], float (&ls)[QT][4], u32x4 (&p)[QT][2],
+                                               float (&alpha)[QT]) {
     f32x16 (&sp)[QT] = s[PB];
     if constexpr (T < 4) {
       constexpr int qt = T >> 1, r0 = 8 * (T & 1);
@@ -224,15 +238,14 @@ struct Flash {
       for (int qt = 0; qt < QT; ++qt) {
         mn[qt] = max_with_partner(mx[qt]) * C::SL;
         need[qt] = mn[qt] > m[qt] + 8.0f;
+        alpha[qt] = 1.0f;
       }
       if (__any(need[0] || need[1])) {
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-          const float alpha = need[qt] ? __builtin_amdgcn_exp2f(m[qt] - mn[qt]) : 1.0f;
+          alpha[qt] = need[qt] ? __builtin_amdgcn_exp2f(m[qt] - mn[qt]) : 1.0f;
           m[qt] = need[qt] ? mn[qt] : m[qt];
-          l[qt] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < DTN; ++dt) o[qt][dt] *= alpha;
+          l[qt] *= alpha[qt];
         }
       }
 #pragma unroll
@@ -252,10 +265,10 @@ struct Flash {
     }
   }
 
-  // Phase A of block j (scores into set SB from stage ST) with the softmax of set PB when PREV.
+  // Scores of one block into set SB from K stage ST, with the softmax of set PB when PREV.
   template <int ST, int SB, int PB, bool PREV>
-  __device__ __forceinline__ void scores(long kprev0, u32x4 (&p)[QT][2]) {
-    const u16_t* kl = ks[ST];
+  __device__ __forceinline__ void scores(long kprev0, u32x4 (&p)[QT][2], float (&alpha)[QT]) {
+    const u16_t* kl = sh.ks[ST];
     float mx[QT], msub[QT], ls[QT][4];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -273,7 +286,7 @@ struct Flash {
       s[SB][qt] = gemm::mfma32x32x16<C::DT>(a, qf[qt][dd], s[SB][qt]);
       if constexpr (qt == 1) a = an;
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (PREV) softmax_slot<PB, t>(mx, msub, ls, p);
+      if constexpr (PREV) softmax_slot<PB, t>(mx, msub, ls, p, alpha);
       __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (PREV) {
@@ -282,35 +295,9 @@ struct Flash {
     }
   }
 
-  // Phase B: O^T += V^T P^T for the block whose V tile is in stage VST.
-  template <int VST>
-  __device__ __forceinline__ void pv(const u32x4 (&p)[QT][2]) {
-    const u16_t* vl = vs[VST];
-    u32x4 a = v_frag(vl, 0, 0, lane), an = a;
-    For<0, 16>::run([&](auto ti) {
-      constexpr int t = decltype(ti)::value, dt = t >> 2, st = (t >> 1) & 1, qt = t & 1;
-      if constexpr (qt == 0 && t + 2 < 16) an = v_frag(vl, (t + 2) >> 2, ((t + 2) >> 1) & 1, lane);
-      o[qt][dt] = gemm::mfma32x32x16<C::DT>(a, p[qt][st], o[qt][dt]);
-      if constexpr (qt == 1) a = an;
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  }
-
-  // Iteration j >= 1 on stage ST = j % 4.
-  template <int ST>
-  __device__ __forceinline__ void iteration(long j, long nkb) {
-    if (j + 1 < nkb) gemm::wait_vmcnt<PER>();
-    else gemm::wait_vmcnt<0>();
-    gemm::lds_reads_done_barrier();
-    if (j + 2 < nkb) issue<(ST + 2) & 3>(j + 2);
-    u32x4 p[QT][2];
-    scores<ST, ST & 1, (ST + 1) & 1, true>((j - 1) * BK, p);
-    pv<(ST + 3) & 3>(p);
-  }
-
-  // Softmax and P.V of the last block, in set PB and stage VST (no scores to overlap with).
-  template <int PB, int VST>
-  __device__ __forceinline__ void last(long k0) {
+  // Softmax of the last block (set PB), with no scores to overlap with.
+  template <int PB>
+  __device__ __forceinline__ void softmax_only(long k0, u32x4 (&p)[QT][2], float (&alpha)[QT]) {
     if constexpr (C::CAUSAL) mask<PB>(k0);
     float mx[QT], msub[QT], ls[QT][4];
 #pragma unroll
@@ -320,103 +307,230 @@ struct Flash {
 #pragma unroll
       for (int i = 0; i < 4; ++i) ls[qt][i] = 0.0f;
     }
-    u32x4 p[QT][2];
-    For<0, 16>::run([&](auto ti) { softmax_slot<PB, decltype(ti)::value>(mx, msub, ls, p); });
+    For<0, 16>::run([&](auto ti) { softmax_slot<PB, decltype(ti)::value>(mx, msub, ls, p, alpha); });
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) l[qt] += (ls[qt][0] + ls[qt][1]) + (ls[qt][2] + ls[qt][3]);
-    pv<VST>(p);
+  }
+
+  // P and the rescale factors of one block into buffer PBUF (lane-linear, conflict-free).
+  template <int PBUF>
+  __device__ __forceinline__ void publish(const u32x4 (&p)[QT][2], const float (&alpha)[QT]) {
+    u32x4* pw = sh.pb + (PBUF * WAVES + wave) * (QT * 2 * 64) + lane;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) pw[(qt * 2 + st) * 64] = p[qt][st];
+    float* aw = sh.ab + ((PBUF * WAVES + wave) * 64 + lane) * QT;
+    *(f32x2*)aw = f32x2{alpha[0], alpha[1]};
+  }
+
+  // Step t (1 <= t < nkb) on K stage ST = t % 4.
+  template <int ST>
+  __device__ __forceinline__ void step(long t, long nkb) {
+    if (t + 1 < nkb) gemm::wait_vmcnt<PER>();
+    else gemm::wait_vmcnt<0>();
+    gemm::lds_reads_done_barrier();
+    if (t + 2 < nkb) load_k<WAVES, C::K_S>(kb, (t + 2) * BK, sh.ks[(ST + 2) & 3], wave, lane);
+    u32x4 p[QT][2];
+    float alpha[QT];
+    scores<ST, ST & 1, (ST + 1) & 1, true>((t - 1) * BK, p, alpha);
+    publish<(ST + 1) & 1>(p, alpha);
+  }
+
+  // Step nkb: the softmax of the last block (index nkb - 1, score set and buffer PB).
+  template <int PB>
+  __device__ __forceinline__ void last_step(long nkb) {
+    gemm::lds_reads_done_barrier();
+    u32x4 p[QT][2];
+    float alpha[QT];
+    softmax_only<PB>((nkb - 1) * BK, p, alpha);
+    publish<PB>(p, alpha);
+  }
+
+  __device__ __forceinline__ void run(const u16_t* __restrict__ qp, long nkb) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int dd = 0; dd < DS; ++dd) qf[qt][dd] = *(const u32x4*)(qp + query(qt) * C::Q_S + 16 * dd + 8 * (lane >> 5));
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      m[qt] = -__builtin_inff();
+      l[qt] = 0.0f;
+    }
+    load_k<WAVES, C::K_S>(kb, 0, sh.ks[0], wave, lane);
+    if (nkb > 1) load_k<WAVES, C::K_S>(kb, BK, sh.ks[1], wave, lane);
+    // Step 0: scores of block 0 only.
+    if (nkb > 1) gemm::wait_vmcnt<PER>();
+    else gemm::wait_vmcnt<0>();
+    gemm::lds_reads_done_barrier();
+    if (nkb > 2) load_k<WAVES, C::K_S>(kb, 2 * BK, sh.ks[2], wave, lane);
+    {
+      u32x4 unused_p[QT][2];
+      float unused_a[QT];
+      scores<0, 0, 1, false>(0, unused_p, unused_a);
+    }
+    long t = 1;
+    for (; t + 3 < nkb; t += 4) {
+      step<1>(t, nkb);
+      step<2>(t + 1, nkb);
+      step<3>(t + 2, nkb);
+      step<0>(t + 3, nkb);
+    }
+    if (t < nkb) step<1>(t, nkb);
+    if (t + 1 < nkb) step<2>(t + 1, nkb);
+    if (t + 2 < nkb) step<3>(t + 2, nkb);
+    if ((nkb - 1) & 1) last_step<1>(nkb);
+    else last_step<0>(nkb);
+    // Row sums (both lanes of a query) for the accumulator's epilogue, then step nkb + 1.
+    float* lw = sh.lb + (wave * 64 + lane) * QT;
+    *(f32x2*)lw = f32x2{sum_with_partner(l[0]), sum_with_partner(l[1])};
+    gemm::lds_reads_done_barrier();
   }
 };
 
 template <class C>
+struct Accumulator {
+  static constexpr int WAVES = C::WAVES, QT = 2, DTN = HD / 32;
+  static constexpr int PER = 8 / WAVES;  // V load instructions per wave per key block
+
+  Lds<C> sh;
+  const u16_t* __restrict__ vb;
+  f32x16 o[QT][DTN];
+  long q0;
+  int wave, lane;
+
+  __device__ __forceinline__ long query(int qt) const { return q0 + 32 * (qt * WAVES + wave) + (lane & 31); }
+
+  // O^T = alpha O^T + V^T P^T for the block in P buffer PBUF and V stage VST.
+  template <int PBUF, int VST>
+  __device__ __forceinline__ void consume() {
+    const u32x4* pr = sh.pb + (PBUF * WAVES + wave) * (QT * 2 * 64) + lane;
+    const f32x2 al = *(const f32x2*)(sh.ab + ((PBUF * WAVES + wave) * 64 + lane) * QT);
+    u32x4 p[QT][2];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) p[qt][st] = pr[(qt * 2 + st) * 64];
+    const u16_t* vl = sh.vs[VST];
+    u32x4 vf[DTN][2];
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) vf[dt][st] = v_frag(vl, dt, st, lane);
+    if (__any(al.x != 1.0f || al.y != 1.0f)) {
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt) {
+        o[0][dt] *= al.x;
+        o[1][dt] *= al.y;
+      }
+    }
+    For<0, 16>::run([&](auto ti) {
+      constexpr int t = decltype(ti)::value, dt = t >> 2, st = (t >> 1) & 1, qt = t & 1;
+      o[qt][dt] = gemm::mfma32x32x16<C::DT>(vf[dt][st], p[qt][st], o[qt][dt]);
+    });
+  }
+
+  // Step t >= 2 on stage ST = t % 4: V(t) is issued, block t - 2 consumed.
+  template <int ST>
+  __device__ __forceinline__ void step(long t, long nkb) {
+    if (t - 1 < nkb) gemm::wait_vmcnt<PER>();
+    else gemm::wait_vmcnt<0>();
+    gemm::lds_reads_done_barrier();
+    if (t < nkb) load_v<WAVES, C::V_S>(vb, t * BK, sh.vs[ST], wave, lane);
+    consume<ST & 1, (ST + 2) & 3>();
+  }
+
+  __device__ __forceinline__ void run(u16_t* __restrict__ out, long b, long nkb) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt) o[qt][dt] = f32x16{};
+    // Steps 0 and 1: V(0) and V(1) are issued.
+    gemm::lds_reads_done_barrier();
+    load_v<WAVES, C::V_S>(vb, 0, sh.vs[0], wave, lane);
+    gemm::lds_reads_done_barrier();
+    if (nkb > 1) load_v<WAVES, C::V_S>(vb, BK, sh.vs[1], wave, lane);
+    // Steps 2 .. nkb + 1.
+    long t = 2;
+    for (; t + 3 <= nkb + 1; t += 4) {
+      step<2>(t, nkb);
+      step<3>(t + 1, nkb);
+      step<0>(t + 2, nkb);
+      step<1>(t + 3, nkb);
+    }
+    if (t <= nkb + 1) step<2>(t, nkb);
+    if (t + 1 <= nkb + 1) step<3>(t + 1, nkb);
+    if (t + 2 <= nkb + 1) step<0>(t + 2, nkb);
+
+    const f32x2 lsum = *(const f32x2*)(sh.lb + (wave * 64 + lane) * QT);
+    const float inv[QT] = {1.0f / lsum.x, 1.0f / lsum.y};
+    const int h = lane >> 5;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      u16_t* __restrict__ orow = out + (b * C::SQ + query(qt)) * HD;
+#pragma unroll
+      for (int dt = 0; dt < DTN; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x16& acc = o[qt][dt];
+          const u32_t lo = pack2<C::DT>(acc[4 * g] * inv[qt], acc[4 * g + 1] * inv[qt]);
+          const u32_t hi = pack2<C::DT>(acc[4 * g + 2] * inv[qt], acc[4 * g + 3] * inv[qt]);
+          *(u32x2*)(orow + dt * 32 + 8 * g + 4 * h) = u32x2{lo, hi};
+        }
+    }
+  }
+};
+
+// Workgroup of 2 * C::WAVES waves (128 * C::WAVES threads) over 64 * C::WAVES queries of one batch
+// index.
+template <class C>
 __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
                                       const u16_t* __restrict__ V, u16_t* __restrict__ O) {
-  using F = Flash<C>;
+  constexpr int WAVES = C::WAVES, QT = 2;
+  constexpr long BQ = 64 * WAVES, NQB = C::SQ / BQ, NKB = C::SK / BK;
+  static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
   __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
   __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
+  __shared__ __attribute__((aligned(16))) u32x4 pbuf[2 * WAVES * QT * 2 * 64];
+  __shared__ __attribute__((aligned(16))) float abuf[2 * WAVES * 64 * QT];
+  __shared__ __attribute__((aligned(16))) float lbuf[WAVES * 64 * QT];
   u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
   u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
+  const Lds<C> sh{ks, vs, pbuf, abuf, lbuf};
 
   // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
   // query blocks with the most keys start first.
   const long total = (long)gridDim.x;
   long t = (long)blockIdx.x;
   if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
-  const long b = t / F::NQB;
-  long qb = t % F::NQB;
-  if constexpr (C::CAUSAL) qb = F::NQB - 1 - qb;
-
-  F f;
-  f.ks = ks;
-  f.vs = vs;
-  f.wave = (int)(threadIdx.x >> 6);
-  f.lane = (int)(threadIdx.x & 63);
-  f.q0 = qb * F::BQ;
-  f.kb = K + C::k_off(b);
-  f.vb = V + C::v_off(b);
-  const u16_t* __restrict__ qb_ptr = Q + C::q_off(b);
-#pragma unroll
-  for (int qt = 0; qt < F::QT; ++qt)
-#pragma unroll
-    for (int dd = 0; dd < F::DS; ++dd)
-      f.qf[qt][dd] = *(const u32x4*)(qb_ptr + f.query(qt) * C::Q_S + 16 * dd + 8 * (f.lane >> 5));
-#pragma unroll
-  for (int qt = 0; qt < F::QT; ++qt) {
-    f.m[qt] = -__builtin_inff();
-    f.l[qt] = 0.0f;
-#pragma unroll
-    for (int dt = 0; dt < F::DTN; ++dt) f.o[qt][dt] = f32x16{};
-  }
-
-  long nkb = F::NKB;
+  const long b = t / NQB;
+  long qb = t % NQB;
+  if constexpr (C::CAUSAL) qb = NQB - 1 - qb;
+  const long q0 = qb * BQ;
+  long nkb = NKB;
   if constexpr (C::CAUSAL) {
-    const long last = (f.q0 + F::BQ - 1) / BK + 1;
+    const long last = (q0 + BQ - 1) / BK + 1;
     nkb = last < nkb ? last : nkb;
   }
-  f.template issue<0>(0);
-  if (nkb > 1) f.template issue<1>(1);
-  // Block 0: scores only.
-  {
-    if (nkb > 1) gemm::wait_vmcnt<F::PER>();
-    else gemm::wait_vmcnt<0>();
-    gemm::lds_reads_done_barrier();
-    if (nkb > 2) f.template issue<2>(2);
-    u32x4 unused[F::QT][2];
-    f.template scores<0, 0, 1, false>(0, unused);
-  }
-  long j = 1;
-  for (; j + 3 < nkb; j += 4) {
-    f.template iteration<1>(j, nkb);
-    f.template iteration<2>(j + 1, nkb);
-    f.template iteration<3>(j + 2, nkb);
-    f.template iteration<0>(j + 3, nkb);
-  }
-  if (j < nkb) f.template iteration<1>(j, nkb);
-  if (j + 1 < nkb) f.template iteration<2>(j + 1, nkb);
-  if (j + 2 < nkb) f.template iteration<3>(j + 2, nkb);
-  // The last block (index nkb - 1) still needs its softmax and P.V.
-  const long lb = nkb - 1;
-  switch (lb & 3) {
-    case 0: f.template last<0, 0>(lb * BK); break;
-    case 1: f.template last<1, 1>(lb * BK); break;
-    case 2: f.template last<0, 2>(lb * BK); break;
-    default: f.template last<1, 3>(lb * BK); break;
-  }
-
-  const int h = f.lane >> 5;
-#pragma unroll
-  for (int qt = 0; qt < F::QT; ++qt) {
-    const float inv = 1.0f / sum_with_partner(f.l[qt]);
-    u16_t* __restrict__ orow = O + (b * C::SQ + f.query(qt)) * HD;
-#pragma unroll
-    for (int dt = 0; dt < F::DTN; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x16& acc = f.o[qt][dt];
-        const u32_t lo = pack2<C::DT>(acc[4 * g] * inv, acc[4 * g + 1] * inv);
-        const u32_t hi = pack2<C::DT>(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
-        *(u32x2*)(orow + dt * 32 + 8 * g + 4 * h) = u32x2{lo, hi};
-      }
+  // The wave index is uniform across the wave; readfirstlane lets the compiler branch on the role.
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int lane = (int)(threadIdx.x & 63);
+  if (w < WAVES) {
+    Scorer<C> f;
+    f.sh = sh;
+    f.kb = K + C::k_off(b);
+    f.q0 = q0;
+    f.wave = w;
+    f.lane = lane;
+    f.run(Q + C::q_off(b), nkb);
+  } else {
+    Accumulator<C> f;
+    f.sh = sh;
+    f.vb = V + C::v_off(b);
+    f.q0 = q0;
+    f.wave = w - WAVES;
+    f.lane = lane;
+    f.run(O, b, nkb);
   }
 }
 

@@ -27,10 +27,10 @@ struct CheckAttnCausalBf16 {
   static __device__ __forceinline__ long v_off(long b) { return (b / 16) * 4194304L + (b % 16) * 128L; }
 };
 
-extern "C" __global__ void __launch_bounds__(256) accy_check_attention_f16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
+extern "C" __global__ void __launch_bounds__(512) accy_check_attention_f16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
   accy::attn::flash<CheckAttnF16>(q, k, v, o);
 }
 
-extern "C" __global__ void __launch_bounds__(256) accy_check_attention_causal_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
+extern "C" __global__ void __launch_bounds__(512) accy_check_attention_causal_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
   accy::attn::flash<CheckAttnCausalBf16>(q, k, v, o);
 }

@@ -1093,13 +1093,13 @@ class Planner {
       params += "const u16_t* __restrict__ " + x + ", ";
     }
     params += "u16_t* __restrict__ " + o;
-    src << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << nm << "(" << params
+    src << "extern \"C\" __global__ void __launch_bounds__(" << 128 * waves << ") " << nm << "(" << params
         << ") {\n  accy::attn::flash<Cfg_" << nm << ">(" << q << ", " << k << ", " << v << ", " << o << ");\n}\n";
     KernelStep ks;
     ks.source = src.str();
     ks.name = nm;
     ks.grid[0] = (uint32_t)(L.nb * (L.sq / (64 * waves)));
-    ks.block[0] = 64 * waves;
+    ks.block[0] = 128 * waves;  // a scorer and an accumulator wave per 64 queries
     ks.klass = "attention";
     ks.label = "attention:%" + std::to_string(pv);
     // Score pairs actually needed: all of them, or those with key <= query under the causal mask.

@@ -38,6 +38,10 @@ template <typename I> __device__ __forceinline__ void st_bf16(u16_t* __restrict_
 template <typename T, typename I> __device__ __forceinline__ T ld(const T* __restrict__ p, I i) { return p[i]; }
 template <typename T, typename I> __device__ __forceinline__ void st(T* __restrict__ p, I i, T v) { p[i] = v; }
 template <typename I> __device__ __forceinline__ bool ld_i1(const u8_t* __restrict__ p, I i) { return p[i] != 0; }
+// Four consecutive elements read as one vector load (the row kernels load each input's four elements
+// of a thread this way at the top of an iteration); alignment capped at the 16 bytes every buffer
+// base guarantees.
+template <typename T> struct alignas(4 * sizeof(T) < 16 ? 4 * sizeof(T) : 16) Quad { T v[4]; };
 template <typename I> __device__ __forceinline__ void st_i1(u8_t* __restrict__ p, I i, bool v) { p[i] = v ? 1 : 0; }
 
 // ---- f32 transcendentals used by generated kernels ----
@@ -92,14 +96,38 @@ __device__ __forceinline__ float sincos_core(float r, int q) {
   return __builtin_bit_cast(float, __builtin_bit_cast(u32_t, v) ^ ((u32_t)(q & 2) << 30));
 }
 
+// sin with one polynomial: x = k pi + r, k = rint(x / pi) read off the low mantissa bits of
+// x / pi + 1.5 * 2^23 (so the sign (-1)^k needs no integer conversion, and k = +0 for x = -0),
+// r = x - k pi by the three-part reduction with FMAs, then the odd Taylor polynomial of sin through
+// r^13 on [-pi/2, pi/2] (truncation below 7e-10) and the sign.
+// The library's reductions for |x| >= 2^17, out of line so that their code does not sit between the
+// loads and arithmetic of every element that takes the fast path (`const`: no memory effects, so
+// loads still move and merge across the calls).
+__device__ __attribute__((noinline, const)) float sin_large(float x) { return sinf(x); }
+__device__ __attribute__((noinline, const)) float cos_large(float x) { return cosf(x); }
+
 __device__ __forceinline__ float sin_f32(float x) {
-  const float P1 = 0x1.921fb6p+0f, P2 = -0x1.777a5cp-25f, P3 = -0x1.ee59dap-50f;
-  const float k = __builtin_rintf(x * 0x1.45f306p-1f);
+  const float M = 0x1.8p+23f;
+  // pi = P1 + P2 + P3 + O(2^-74 pi), every part positive (P1, P2 rounded down), so that x = -0 keeps
+  // r = -0 through all three FMAs.
+  const float P1 = 0x1.921fb4p+1f, P2 = 0x1.4442d0p-23f, P3 = 0x1.84698ap-47f;
+  const float t = __builtin_fmaf(x, 0x1.45f306p-2f, M);
+  const float k = t - M;
   float r = __builtin_fmaf(-k, P1, x);
   r = __builtin_fmaf(-k, P2, r);
   r = __builtin_fmaf(-k, P3, r);
-  float v = sincos_core(r, (int)k);
-  if (__builtin_fabsf(x) >= 0x1p+17f) v = sinf(x);
+  const float r2 = r * r;
+  float p = __builtin_fmaf(r2, 0x1.612462p-33f, -0x1.ae6456p-26f);  // 1/13!, -1/11!
+  p = __builtin_fmaf(r2, p, 0x1.71de3ap-19f);                        // 1/9!
+  p = __builtin_fmaf(r2, p, -0x1.a01a02p-13f);                       // -1/7!
+  p = __builtin_fmaf(r2, p, 0x1.111112p-7f);                         // 1/5!
+  p = __builtin_fmaf(r2, p, -0x1.555556p-3f);                        // -1/3!
+  // sin r has the sign of r on [-pi/2, pi/2]; or-ing r's sign bit in only matters for r = -0 (the
+  // FMA turns it into +0).
+  const float s = __builtin_fmaf(r * r2, p, r);
+  const u32_t sb = __builtin_bit_cast(u32_t, s) | (__builtin_bit_cast(u32_t, r) & 0x80000000u);
+  float v = __builtin_bit_cast(float, sb ^ (__builtin_bit_cast(u32_t, t) << 31));
+  if (__builtin_fabsf(x) >= 0x1p+17f) v = sin_large(x);
   return v;
 }
 
@@ -110,7 +138,7 @@ __device__ __forceinline__ float cos_f32(float x) {
   r = __builtin_fmaf(-k, P2, r);
   r = __builtin_fmaf(-k, P3, r);
   float v = sincos_core(r, (int)k + 1);
-  if (__builtin_fabsf(x) >= 0x1p+17f) v = cosf(x);
+  if (__builtin_fabsf(x) >= 0x1p+17f) v = cos_large(x);
   return v;
 }
 

@@ -205,6 +205,21 @@ std::string KernelWriter::load_at(int slot, const std::string& base, const std::
   }
 }
 
+std::string KernelWriter::quad_load(int slot, const std::string& var, const std::string& base, DType d) {
+  const std::string q = std::string("accy::Quad<") + storage_type(d) + ">";
+  return "const " + q + " " + var + " = *(const " + q + "*)(" + arg(slot, false) + " + " + base + ");";
+}
+
+std::string KernelWriter::quad_elem(const std::string& var, const std::string& idx, DType d) {
+  const std::string e = var + ".v[" + idx + "]";
+  switch (d) {
+    case DType::f16: return "accy::f16_to_f32(" + e + ")";
+    case DType::bf16: return "accy::bf16_to_f32(" + e + ")";
+    case DType::i1: return "(" + e + " != 0)";
+    default: return e;
+  }
+}
+
 std::string KernelWriter::store(int slot, const std::string& off, DType d, const std::string& v) {
   std::string a = arg(slot, true);
   switch (d) {

@@ -63,6 +63,10 @@ class KernelWriter {
   std::string load(int slot, const std::string& off, DType d);
   // Load of element `idx` past `base` (pointer-base form, so adjacent idx merge into vector loads).
   std::string load_at(int slot, const std::string& base, const std::string& idx, DType d);
+  // Declaration of an aligned four-element load of slot at element offset base (an accy::Quad), and
+  // element idx of such a variable converted to the compute type.
+  std::string quad_load(int slot, const std::string& var, const std::string& base, DType d);
+  static std::string quad_elem(const std::string& var, const std::string& idx, DType d);
   std::string store(int slot, const std::string& off, DType d, const std::string& v);
   std::string tmp();
   std::string params() const;

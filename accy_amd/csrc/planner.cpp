@@ -6,6 +6,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <optional>
 #include <set>
 #include <sstream>
 
@@ -416,9 +417,10 @@ class Planner {
     std::map<std::string, std::set<int>> use_record;
     // A load whose offset is `rest + c` (c the row's element index, rank-1 row) is written as
     // (ptr + rest + c0)[u] so that the VEC adjacent loads of one thread merge into one vector load.
-    auto direct_load = [&](int slot, const std::string& off, DType d) -> std::string {
+    // The `rest` of an offset `(rest + c)` (empty optional when the offset has another form).
+    auto row_rest = [&](const std::string& off) -> std::optional<std::string> {
       if (VEC == 1 || tc.size() != 1 || tc[0] != "c" || off.size() < 2 || off.front() != '(' || off.back() != ')')
-        return w.load(slot, off, d);
+        return std::nullopt;
       std::string body = off.substr(1, off.size() - 2), rest;
       bool found = false;
       size_t pos = 0;
@@ -432,14 +434,25 @@ class Planner {
           if (term[i] == 'c' && ident_start && ident_end) has_c = true;
         }
         if (term == "c" && !found) found = true;
-        else if (has_c) return w.load(slot, off, d);
+        else if (has_c) return std::nullopt;
         else rest += (rest.empty() ? "" : " + ") + term;
         if (nx == std::string::npos) break;
         pos = nx + 3;
       }
-      if (!found) return w.load(slot, off, d);
-      return w.load_at(slot, "(" + (rest.empty() ? std::string("0") : rest) + ") + c0", "u", d);
+      if (!found) return std::nullopt;
+      return "(" + (rest.empty() ? std::string("0") : rest) + ") + c0";
     };
+    auto direct_load = [&](int slot, const std::string& off, DType d) -> std::string {
+      const std::optional<std::string> base = row_rest(off);
+      return base ? w.load_at(slot, *base, "u", d) : w.load(slot, off, d);
+    };
+    // Without a tail guard, a leaf read at `rest + c` is loaded for the thread's VEC elements at once,
+    // at the top of the element iteration (one aligned vector load per input, issued before any of
+    // the iteration's arithmetic), and each element takes its lane.
+    const bool hoist = VEC == 4 && !guard;
+    std::string hoisted;
+    std::map<std::string, std::string> hoisted_var;
+    int nquad = 0;
     w.leaf_hook = [&](int slot, const std::string& off, DType d, Scope& sc, std::string& out) -> bool {
       bool varies = false;
       for (const auto& t : tc)
@@ -450,7 +463,20 @@ class Planner {
       auto it = leaf_array.find(key);
       if (it == leaf_array.end()) {
         std::string t = w.tmp();
-        sc.out << sc.indent << "const " << compute_type(d) << " " << t << " = " << direct_load(slot, off, d) << ";\n";
+        std::optional<std::string> base = hoist ? row_rest(off) : std::nullopt;
+        std::string val;
+        if (base) {
+          auto hv = hoisted_var.find(key);
+          if (hv == hoisted_var.end()) {
+            std::string q = "q" + std::to_string(nquad++);
+            hoisted += "      " + w.quad_load(slot, q, *base, d) + "\n";
+            hv = hoisted_var.emplace(key, q).first;
+          }
+          val = KernelWriter::quad_elem(hv->second, "u", d);
+        } else {
+          val = direct_load(slot, off, d);
+        }
+        sc.out << sc.indent << "const " << compute_type(d) << " " << t << " = " << val << ";\n";
         out = t;
         return true;
       }
@@ -477,17 +503,31 @@ class Planner {
       return false;
     };
     std::ostringstream body;
-    std::string loop_head;
+    // Element loop: fully unrolled when the thread's elements are cached in registers across passes;
+    // otherwise unrolled by a few iterations (all of them would keep every hoisted load live at
+    // once), ACCY_ROW_UNROLL overriding the factor.
+    std::string unroll = cache ? "#pragma unroll\n" : (unrolled ? "#pragma unroll 4\n" : "#pragma unroll 2\n");
+    if (!cache) {
+      if (const char* e = std::getenv("ACCY_ROW_UNROLL")) unroll = std::string("#pragma unroll ") + e + "\n";
+    }
+    std::string loop_head_a, loop_head_b;
     {
-      std::ostringstream lh;
-      lh << (unrolled ? "#pragma unroll\n" : "#pragma unroll 2\n") << "    for (int e = 0; e < " << E << "; ++e) {\n"
-         << "      const I c0 = ((I)e * " << B << " + (I)threadIdx.x) * " << VEC << ";\n"
-         << "#pragma unroll\n"
+      std::ostringstream la, lb;
+      la << unroll << "    for (int e = 0; e < " << E << "; ++e) {\n"
+         << "      const I c0 = ((I)e * " << B << " + (I)threadIdx.x) * " << VEC << ";\n";
+      lb << "#pragma unroll\n"
          << "      for (int u = 0; u < " << VEC << "; ++u) {\n"
          << "        const I c = c0 + u;\n";
-      if (guard) lh << "        if (c < (I)" << tn << ") {\n";
-      loop_head = lh.str();
+      if (guard) lb << "        if (c < (I)" << tn << ") {\n";
+      loop_head_a = la.str();
+      loop_head_b = lb.str();
     }
+    // One element loop: head, the pass's hoisted loads, per-element code, tail.
+    auto emit_loop = [&](const std::string& inner_code, const std::string& tail) {
+      body << loop_head_a << hoisted << loop_head_b << inner_code << tail;
+      hoisted.clear();
+      hoisted_var.clear();
+    };
     std::string loop_tail = guard ? "        }\n      }\n    }\n" : "      }\n    }\n";
     std::string lds_decl;
     for (size_t j = 0; j < rk.reduces.size(); ++j) {
@@ -500,11 +540,11 @@ class Planner {
       std::string init = w.value(op.args[1], {}, pre);
       std::string acc = "acc" + std::to_string(j);
       body << "    " << at << " " << acc << " = (" << at << ")" << init << ";\n";
-      body << loop_head;
-      Scope inner(body, guard ? "          " : "        ");
+      std::ostringstream ib;
+      Scope inner(ib, guard ? "          " : "        ");
       std::string x = w.value(op.args[0], full, inner);
-      body << inner.indent << acc << " = " << fold_step(d, r, acc, x) << ";\n";
-      body << loop_tail;
+      ib << inner.indent << acc << " = " << fold_step(d, r, acc, x) << ";\n";
+      emit_loop(ib.str(), loop_tail);
       std::string lds = "lds" + std::to_string(j);
       lds_decl += "  __shared__ " + at + " " + lds + "[" + std::to_string(std::max<uint32_t>(B / 64, 1)) + "];\n";
       body << "    " << acc << " = accy::block_reduce<" << B << ">(" << acc << ", " << reducer_op(r) << ", " << lds
@@ -526,13 +566,13 @@ class Planner {
     }
     if (!rk.full_vals.empty()) {
       cur_pass = (int)rk.reduces.size();
-      body << loop_head;
-      Scope sc(body, guard ? "          " : "        ");
+      std::ostringstream ib;
+      Scope sc(ib, guard ? "          " : "        ");
       for (uint32_t v : rk.full_vals) {
         std::string x = w.value(v, full, sc);
-        if (commit) body << sc.indent << w.store(slots_.slot_of[v], "row * (I)" + std::to_string(tn) + " + c", g_.type(v).dtype, x) << "\n";
+        if (commit) ib << sc.indent << w.store(slots_.slot_of[v], "row * (I)" + std::to_string(tn) + " + c", g_.type(v).dtype, x) << "\n";
       }
-      body << loop_tail;
+      emit_loop(ib.str(), loop_tail);
     }
     probe_use_ = use_record;
     KernelStep k;

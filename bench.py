@@ -58,7 +58,10 @@ def measured_traffic(config: str, label: str):
 
 
 VALU = Path(__file__).resolve().parent / "profiles" / "valu.json"
-VALU_ISSUE_PEAK = 256 * 2.4e9  # wave64 VALU instructions per second: one per CU per clock
+# Wave64 VALU instructions per second at the published FP32 vector peak: 157.3 TFLOP/s is 2 FLOP x 64
+# lanes x 2 FMA instructions per CU per clock (256 CUs at 2.4 GHz); two waves on a SIMD reach about
+# that rate with independent FMAs.
+VALU_ISSUE_PEAK = 2 * 256 * 2.4e9
 
 
 def measured_valu(config: str, label: str):

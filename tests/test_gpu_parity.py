@@ -420,6 +420,42 @@ def test_device_tanh_against_float64():
     assert tail[3] == 0.0 and np.signbit(tail[3]) and tail[4] == 0.0 and not np.signbit(tail[4])
 
 
+def _ulp_error(got, ref):
+    """|got - ref| in units of the f32 spacing at the float64 result."""
+    spacing = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - ref) / np.maximum(spacing, np.float64(2.0 ** -149))
+
+
+@pytest.mark.parametrize("fn", ["sin", "cos"])
+def test_device_sin_cos_against_float64(fn):
+    """accy::sin_f32 / cos_f32: within 2 ulp of the float64 value for |x| < 2^17 (dense sweeps, random
+    arguments, the float32 neighbours of multiples of pi/2), the library's reduction beyond, sin(-0) =
+    -0, and NaN for infinities and NaN."""
+    rng = np.random.default_rng(77)
+    near = (np.arange(-4000, 4001) * (np.pi / 2)).astype(np.float32)
+    x = np.concatenate([np.linspace(-20, 20, 40001), rng.uniform(-2.0 ** 17, 2.0 ** 17, 40000),
+                        rng.uniform(-100, 100, 20000), near, np.nextafter(near, np.float32(np.inf)),
+                        np.nextafter(near, np.float32(-np.inf)), np.geomspace(1e-30, 1, 2000),
+                        -np.geomspace(1e-30, 1, 2000)]).astype(np.float32)
+    x = x[np.abs(x) < 2.0 ** 17]
+    big = np.array([2.0 ** 17, -2.0 ** 17, 1e6, -3.5e7, 1e30], np.float32)
+    special = np.array([np.inf, -np.inf, np.nan, -0.0, 0.0], np.float32)
+    xs = np.concatenate([x, big, special])
+    prog = T.define(fn, [T.spec("f32", i=len(xs))], lambda b, a: getattr(a[0], fn)())
+    got = hip_run(prog, [xs])[0]
+    f64 = getattr(np, fn)
+    err = _ulp_error(got[:len(x)], f64(x.astype(np.float64)))
+    assert err.max() <= 2.0, f"worst {err.max():.2f} ulp at x = {x[err.argmax()]!r}"
+    errb = _ulp_error(got[len(x):len(x) + len(big)], f64(big.astype(np.float64)))
+    assert errb.max() <= 2.0, f"worst {errb.max():.2f} ulp beyond 2^17"
+    tail = got[len(x) + len(big):]
+    assert np.isnan(tail[:3]).all()
+    if fn == "sin":
+        assert tail[3] == 0.0 and np.signbit(tail[3]) and tail[4] == 0.0 and not np.signbit(tail[4])
+    else:
+        assert tail[3] == 1.0 and tail[4] == 1.0
+
+
 # ---- exact classes ----
 
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])

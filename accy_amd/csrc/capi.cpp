@@ -10,6 +10,7 @@
 
 #include "plan.hpp"
 #include "runtime.hpp"
+#include "tuning.hpp"
 #include "wire.hpp"
 
 using namespace accy;
@@ -135,7 +136,9 @@ int accy_hip_compile(const uint8_t* wire_bytes, size_t wire_len, accy_hip_handle
     }
     Plan plan;
     try {
-      plan = lower(prog);
+      LowerOptions opt;
+      opt.tuning = &process_tuning();
+      plan = lower(prog, opt);
     } catch (const Error& e) {
       return fail_with(ACCY_HIP_COMPILE_FAILED, e.what());
     }
@@ -303,7 +306,9 @@ int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile
       return fail_with(e.code == Err::UnsupportedVersion ? ACCY_HIP_UNSUPPORTED_VERSION : ACCY_HIP_INVALID_PROGRAM,
                        e.what());
     }
-    Plan plan = lower(prog);
+    LowerOptions opt;
+    opt.tuning = &process_tuning();
+    Plan plan = lower(prog, opt);
     std::string text;
     for (const Step& st : plan.steps) {
       if (st.type == Step::Copy) {
@@ -312,6 +317,9 @@ int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile
       }
       const KernelStep& k = st.kernel;
       text += "// " + k.label + " grid " + std::to_string(k.grid[0]) + " block " + std::to_string(k.block[0]) + "\n";
+      if (k.candidate_count > 1)
+        text += "// tuning " + k.tuning_key + " candidate " + std::to_string(k.candidate) + " of " +
+                std::to_string(k.candidate_count) + "\n";
       text += k.source;
       if (compile) compile_kernel_source(full_kernel_source(k.source), k.name);
     }
@@ -323,6 +331,60 @@ int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile
     }
     return ACCY_HIP_OK;
   });
+}
+
+int accy_hip_tune(const uint8_t* wire_bytes, size_t wire_len, const void* const* inputs, size_t n_inputs,
+                  void* const* outputs, size_t n_outputs, uint32_t repeats, size_t* n_tuned) {
+  return guarded([&]() -> int {
+    if (n_inputs && !inputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
+    if (n_outputs && !outputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
+    Program prog;
+    try {
+      prog = decode_program(wire_bytes, wire_len);
+    } catch (const Error& e) {
+      return fail_with(e.code == Err::UnsupportedVersion ? ACCY_HIP_UNSUPPORTED_VERSION : ACCY_HIP_INVALID_PROGRAM,
+                       e.what());
+    }
+    size_t n = 0;
+    try {
+      n = tune_program(prog, inputs, n_inputs, outputs, n_outputs, repeats, process_tuning());
+    } catch (const Error& e) {
+      return fail_with(ACCY_HIP_COMPILE_FAILED, e.what());
+    }
+    if (n_tuned) *n_tuned = n;
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_tuning_export(uint8_t* buf, size_t cap, size_t* needed) {
+  return guarded([&]() -> int {
+    const std::vector<uint8_t> bytes = process_tuning().encode();
+    if (needed) *needed = bytes.size();
+    if (buf && cap) {
+      if (cap < bytes.size()) return fail_with(ACCY_HIP_INVALID_BUFFER, "export buffer too small");
+      std::memcpy(buf, bytes.data(), bytes.size());
+    }
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_tuning_import(const uint8_t* data, size_t len) {
+  return guarded([&]() -> int {
+    if (!data && len) return fail_with(ACCY_HIP_INVALID_BUFFER, "null artifact");
+    process_tuning().merge(data, len);
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_tuning_count(size_t* n) {
+  if (!n) return fail_with(ACCY_HIP_INVALID_BUFFER, "null count pointer");
+  *n = process_tuning().size();
+  return ACCY_HIP_OK;
+}
+
+int accy_hip_tuning_clear(void) {
+  process_tuning().clear();
+  return ACCY_HIP_OK;
 }
 
 static int hip_status(hipError_t e, const char* what) {

@@ -8,6 +8,7 @@
 #pragma once
 
 #include <cstdint>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -37,6 +38,12 @@ struct KernelStep {
   std::string klass;         // "map", "row", "fold", "dot", "gemm", "attention", ...
   double algorithmic_bytes = 0;  // HBM bytes the kernel must move (inputs read once, outputs written)
   double algorithmic_flops = 0;  // useful floating-point work
+  // Launch tuning: kernels with more than one launch candidate (results bit-identical across them)
+  // carry a key (device family, class, fingerprint of the default source, shape) and the candidate
+  // this source was generated for (0 = the planner's default).
+  std::string tuning_key;
+  uint32_t candidate_count = 1;
+  uint32_t candidate = 0;
 };
 
 struct CopyStep {
@@ -57,10 +64,16 @@ struct Plan {
   std::vector<int> output_slots;  // per program output
 };
 
+class TuningTable;
+
 struct LowerOptions {
   bool allow_gemm = true;       // MFMA contraction kernels for f32 / f16 / bf16
   bool allow_attention = true;  // fused QK^T -> softmax -> V
   bool allow_row = true;        // fused row pipelines (else serial folds)
+  // Launch candidate per kernel index (the order of the plan's kernel steps), for measuring; a
+  // kernel not listed takes the table's selection for its key, else candidate 0.
+  std::map<size_t, uint32_t> force_candidate;
+  const TuningTable* tuning = nullptr;
 };
 
 // Lowers a decoded program. Throws accy::Error(Unsupported) for operations the target cannot run.

@@ -12,6 +12,7 @@
 
 #include "lower_internal.hpp"
 #include "plan.hpp"
+#include "tuning.hpp"
 
 namespace accy {
 using namespace detail;
@@ -504,12 +505,13 @@ class Planner {
     };
     std::ostringstream body;
     // Element loop: fully unrolled when the thread's elements are cached in registers across passes;
-    // otherwise unrolled by a few iterations (all of them would keep every hoisted load live at
-    // once), ACCY_ROW_UNROLL overriding the factor.
-    std::string unroll = cache ? "#pragma unroll\n" : (unrolled ? "#pragma unroll 4\n" : "#pragma unroll 2\n");
-    if (!cache) {
-      if (const char* e = std::getenv("ACCY_ROW_UNROLL")) unroll = std::string("#pragma unroll ") + e + "\n";
-    }
+    // otherwise unrolled by a few iterations (all of them would keep every hoisted load live at once).
+    // Launch candidates when not cached: the unroll factor (first = default); the source carries a
+    // placeholder until the candidate is chosen.
+    static const char* const kUnrollMark = "#pragma unroll ACCY_ELEMENT_UNROLL\n";
+    const std::vector<int> unroll_candidates =
+        cache ? std::vector<int>{0} : (unrolled ? std::vector<int>{4, 2, 1, 8} : std::vector<int>{2, 1, 4});
+    std::string unroll = cache ? "#pragma unroll\n" : kUnrollMark;
     std::string loop_head_a, loop_head_b;
     {
       std::ostringstream la, lb;
@@ -584,6 +586,14 @@ class Planner {
         << w.align_hints() << lds_decl << "  for (I row = blockIdx.x; row < (I)" << kn << "; row += gridDim.x) {\n"
         << decls << body.str() << "  }\n}\n";
     k.source = src.str();
+    if (unroll_candidates.size() > 1) {
+      k.tuning_key = tuning_key("row", k.source, "rows=" + std::to_string(kn) + ",cols=" + std::to_string(tn));
+      k.candidate_count = (uint32_t)unroll_candidates.size();
+      k.candidate = candidate_for(k.tuning_key, k.candidate_count);
+      const std::string pragma = "#pragma unroll " + std::to_string(unroll_candidates[k.candidate]) + "\n";
+      for (size_t at = k.source.find(kUnrollMark); at != std::string::npos; at = k.source.find(kUnrollMark, at))
+        k.source.replace(at, std::strlen(kUnrollMark), pragma);
+    }
     k.name = nm;
     k.grid[0] = (uint32_t)std::min<uint64_t>(kn, 1u << 20);
     k.block[0] = B;
@@ -594,6 +604,27 @@ class Planner {
   }
 
   std::map<std::string, std::set<int>> probe_use_;
+
+  // ---- launch tuning ----
+  size_t kernel_index() const {
+    size_t n = 0;
+    for (const Step& st : plan_.steps) n += st.type == Step::Kernel ? 1 : 0;
+    return n;
+  }
+  // Key of a tunable kernel: device family, class, fingerprint of its default source and a readable
+  // shape.
+  static std::string tuning_key(const std::string& klass, const std::string& source, const std::string& shape) {
+    return "gfx950/" + klass + "/" + fingerprint(source) + "/" + shape;
+  }
+  // Candidate for the next kernel step: forced (measurement), else the table's selection, else 0.
+  uint32_t candidate_for(const std::string& key, uint32_t count) const {
+    if (count <= 1) return 0;
+    auto f = opt_.force_candidate.find(kernel_index());
+    if (f != opt_.force_candidate.end()) return f->second < count ? f->second : 0;
+    if (opt_.tuning)
+      if (auto sel = opt_.tuning->find(key, count)) return sel->candidate;
+    return 0;
+  }
 
   // ---- strided views: a value that is a transpose / rename / broadcast of a buffer ----
   struct View {
@@ -1337,8 +1368,16 @@ class Planner {
           << ";\n"
           << gs.ga_b.fn("a_b") << gs.ga_m.fn("a_m") << gs.ga_k.fn("a_k") << gs.gb_b.fn("b_b") << gs.gb_k.fn("b_k")
           << gs.gb_n.fn("b_n");
+      // Launch candidates of the direct-to-LDS kernel: the N tile (256, then 128 where B's layout
+      // allows it); the source carries a placeholder until the candidate is chosen.
+      std::vector<int> n_tiles{dn};
+      if (dma && dn == 256) {
+        bool kc2 = bkc;
+        if (dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, 128, kc2) && kc2 == bkc) n_tiles.push_back(128);
+      }
       if (dma) {
-        src << "  static constexpr int BM = " << dm << ", BN = " << dn << ";\n};\n";
+        src << "  static constexpr int BM = " << dm << ", BN = " << (n_tiles.size() > 1 ? "ACCY_N_TILE" : std::to_string(dn))
+            << ";\n};\n";
       } else {
         src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
             << ", WAVES_N = " << WN << ";\n};\n";
@@ -1347,12 +1386,22 @@ class Planner {
       src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(" << w->params() << ") {\n"
           << "  accy::gemm::" << (dma ? "mma16_dma" : "mma16") << "<Cfg_" << nm << ">(" << a << " + " << gs.a.offset
           << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << inits.str() << "});\n}\n";
+      k.source = src.str();
+      if (n_tiles.size() > 1) {
+        k.tuning_key = tuning_key("gemm", k.source, "m=" + std::to_string(gs.m) + ",n=" + std::to_string(gs.n) +
+                                                        ",k=" + std::to_string(gs.k) + ",batch=" + std::to_string(gs.batch));
+        k.candidate_count = (uint32_t)n_tiles.size();
+        k.candidate = candidate_for(k.tuning_key, k.candidate_count);
+        dn = n_tiles[k.candidate];
+        const std::string mark = "ACCY_N_TILE";
+        k.source.replace(k.source.find(mark), mark.size(), std::to_string(dn));
+      }
       int64_t tiles = dma ? (gs.m / dm) * (gs.n / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
       k.grid[0] = (uint32_t)tiles;
       k.block[0] = threads;
       k.shared_bytes = dma ? 0u : 2u * (BM + BN) * (BK + 8) * 2u;
     }
-    k.source = src.str();
+    if (k.source.empty()) k.source = src.str();
     k.name = nm;
     k.grid[1] = (uint32_t)gs.batch;
     k.klass = "gemm";

@@ -93,7 +93,8 @@ EXPORTS = ["accy_hip_run", "accy_hip_compile", "accy_hip_counts", "accy_hip_desc
            "accy_hip_kernel_count", "accy_hip_kernel_info", "accy_hip_plan_source", "accy_hip_device_arch",
            "accy_hip_malloc", "accy_hip_free", "accy_hip_memcpy", "accy_hip_stream_create",
            "accy_hip_stream_destroy", "accy_hip_stream_synchronize", "accy_hip_event_create",
-           "accy_hip_event_destroy", "accy_hip_event_record", "accy_hip_event_elapsed_ms"]
+           "accy_hip_event_destroy", "accy_hip_event_record", "accy_hip_event_elapsed_ms", "accy_hip_tune",
+           "accy_hip_tuning_export", "accy_hip_tuning_import", "accy_hip_tuning_count", "accy_hip_tuning_clear"]
 
 
 def library() -> ctypes.CDLL:
@@ -130,6 +131,11 @@ def library() -> ctypes.CDLL:
         lib.accy_hip_event_destroy.argtypes = [vp]
         lib.accy_hip_event_record.argtypes = [vp, vp]
         lib.accy_hip_event_elapsed_ms.argtypes = [ctypes.POINTER(ctypes.c_float), vp, vp]
+        lib.accy_hip_tune.argtypes = [u8p, sz, vpp, sz, vpp, sz, ctypes.c_uint32, szp]
+        lib.accy_hip_tuning_export.argtypes = [ctypes.POINTER(ctypes.c_uint8), sz, szp]
+        lib.accy_hip_tuning_import.argtypes = [ctypes.POINTER(ctypes.c_uint8), sz]
+        lib.accy_hip_tuning_count.argtypes = [szp]
+        lib.accy_hip_tuning_clear.argtypes = []
         for name in EXPORTS:
             if name != "accy_hip_last_error":
                 getattr(lib, name).restype = ctypes.c_int
@@ -306,6 +312,58 @@ def plan_source(program, compile: bool = False) -> str:
     buf = ctypes.create_string_buffer(need.value)
     _check(lib.accy_hip_plan_source(w, wl, 0, buf, need.value, ctypes.byref(need)))
     return buf.value.decode()
+
+
+# ---- launch tuning (src/executable/tuning.zig: measured candidates, one selection per kernel key) ----
+
+def tune(program, inputs: Sequence[np.ndarray], repeats: int = 20) -> int:
+    """Measures every launch candidate of the program's tunable kernels on the device (inputs copied
+    to HBM first), checks that each candidate's outputs equal the default's byte for byte, and records
+    the fastest candidate per kernel in the process-wide table. Returns the number of kernels tuned."""
+    lib = library()
+    w, wl = _u8(_wire(program))
+    prog = program if isinstance(program, _tensor.Program) else None
+    if prog is None:
+        raise TypeError("tune needs a traced Program (for its output sizes)")
+    ins = [DeviceBuffer.from_array(np.asarray(x)) for x in inputs]
+    outs = [DeviceBuffer(int(np.prod(t.shape, dtype=np.int64)) * np.dtype(_tensor.NUMPY_DTYPE[t.dtype]).itemsize)
+            for t in prog.output_types()]
+    try:
+        ip = (ctypes.c_void_p * max(len(ins), 1))(*[b.ptr for b in ins])
+        op = (ctypes.c_void_p * max(len(outs), 1))(*[b.ptr for b in outs])
+        n = ctypes.c_size_t()
+        _check(lib.accy_hip_tune(w, wl, ip, len(ins), op, len(outs), int(repeats), ctypes.byref(n)))
+        return int(n.value)
+    finally:
+        for b in ins + outs:
+            b.free()
+
+
+def tuning_export() -> bytes:
+    """The process-wide tuning table as an artifact ("ACTT", version 1)."""
+    lib = library()
+    need = ctypes.c_size_t()
+    _check(lib.accy_hip_tuning_export(None, 0, ctypes.byref(need)))
+    buf = (ctypes.c_uint8 * max(need.value, 1))()
+    _check(lib.accy_hip_tuning_export(buf, need.value, ctypes.byref(need)))
+    return bytes(buf[: need.value])
+
+
+def tuning_import(artifact: bytes) -> None:
+    """Merges an artifact into the table (a record replaces one of the same key only when faster)."""
+    data = bytes(artifact)
+    buf = (ctypes.c_uint8 * max(len(data), 1)).from_buffer_copy(data if data else b"\0")
+    _check(library().accy_hip_tuning_import(buf, len(data)))
+
+
+def tuning_count() -> int:
+    n = ctypes.c_size_t()
+    _check(library().accy_hip_tuning_count(ctypes.byref(n)))
+    return int(n.value)
+
+
+def tuning_clear() -> None:
+    _check(library().accy_hip_tuning_clear())
 
 
 def device_arch() -> str:

@@ -118,6 +118,28 @@ int accy_hip_plan_source(const uint8_t* wire, size_t wire_len, int compile, char
 /* Name of the current HIP device's architecture (e.g. "gfx950:sramecc+:xnack-"). */
 int accy_hip_device_arch(char* buf, size_t cap);
 
+/* Launch tuning, the gfx950 counterpart of the reference's launch-tuning cache
+ * (src/executable/tuning.zig:9-289: candidate measurements, one selection per kernel key,
+ * `selectionForKernel`; :291-468 the artifact's encoding).
+ * A tunable kernel (a row kernel's element-loop unroll, a 16-bit contraction's N tile) has a few
+ * launch candidates with bit-identical results; compile and plan_source take the selection recorded
+ * for the kernel's key in the process-wide table (loaded from $ACCY_TUNING_FILE on first use when
+ * set), else the default.
+ * accy_hip_tune: compiles every candidate plan of `wire`, runs each on the device buffers given (as
+ * accy_hip_invoke_device; outputs are overwritten), requires every candidate's outputs to equal the
+ * default's byte for byte (else ACCY_HIP_COMPILE_FAILED), times `repeats` invocations per candidate
+ * and records the fastest per kernel; `*n_tuned` = kernels recorded.
+ * accy_hip_tuning_export: writes the table as an artifact ("ACTT", version 1) into `buf` when `cap`
+ * is large enough; `*needed` = its size. accy_hip_tuning_import: merges an artifact (a record replaces
+ * one of the same key only when faster); a bad magic, version or record leaves the table unchanged
+ * and returns ACCY_HIP_INVALID_PROGRAM or ACCY_HIP_UNSUPPORTED_VERSION. */
+int accy_hip_tune(const uint8_t* wire, size_t wire_len, const void* const* inputs, size_t n_inputs,
+                  void* const* outputs, size_t n_outputs, uint32_t repeats, size_t* n_tuned);
+int accy_hip_tuning_export(uint8_t* buf, size_t cap, size_t* needed);
+int accy_hip_tuning_import(const uint8_t* data, size_t len);
+int accy_hip_tuning_count(size_t* n);
+int accy_hip_tuning_clear(void);
+
 /* Device memory, streams and events of the runtime this library is linked against, for callers
  * that keep inputs and outputs resident in HBM (the buffer half of the backend vtable:
  * allocate_buffer / write_buffer / read_buffer / synchronize / destroy_object,

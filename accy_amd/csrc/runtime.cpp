@@ -237,6 +237,13 @@ void Executor::invoke_device(const void* const* inputs, size_t n_inputs, void* c
                              hipStream_t stream) {
   if (n_inputs != plan_.input_slots.size() || n_outputs != plan_.output_slots.size())
     throw HipFailure(kStatusInvalidBuffer, "buffer count mismatch");
+  // Buffers are used in place and the kernels read and write them with 16-byte vector accesses
+  // (binding.zig:138-200 refuses an imported slice below the backend's minimum alignment).
+  auto aligned = [](const void* p) { return ((uintptr_t)p & (kMinBufferAlignment - 1)) == 0; };
+  for (size_t i = 0; i < n_inputs; ++i)
+    if (!aligned(inputs[i])) throw HipFailure(kStatusInvalidBuffer, "input " + std::to_string(i) + " not 16-byte aligned");
+  for (size_t i = 0; i < n_outputs; ++i)
+    if (!aligned(outputs[i])) throw HipFailure(kStatusInvalidBuffer, "output " + std::to_string(i) + " not 16-byte aligned");
   for (size_t i = 0; i < n_inputs; ++i) bound_[(size_t)plan_.input_slots[i]] = const_cast<void*>(inputs[i]);
   for (size_t i = 0; i < n_outputs; ++i) bound_[(size_t)plan_.output_slots[i]] = outputs[i];
   run_steps(stream);

@@ -6,6 +6,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <cstdint>
 #include <memory>
 #include <string>
 #include <vector>
@@ -24,6 +25,8 @@ struct HipFailure : std::runtime_error {
 constexpr int kStatusOk = 0, kStatusInvalidProgram = 1, kStatusUnsupportedVersion = 2, kStatusInvalidHandle = 3,
               kStatusInvalidBuffer = 4, kStatusTooManyPrograms = 5, kStatusOutOfMemory = 6,
               kStatusCompileFailed = 7, kStatusLaunchFailed = 8;
+// Device buffers passed in place must be aligned to this many bytes (hipMalloc's are).
+constexpr uintptr_t kMinBufferAlignment = 16;
 
 // Compiles one generated kernel source for gfx950 with hiprtc; returns the code object.
 std::vector<char> compile_kernel_source(const std::string& source, const std::string& name);

@@ -94,7 +94,9 @@ int accy_hip_invoke(accy_hip_handle h, const void* const* inputs, const size_t* 
 /* The same launch on device memory already resident in HBM: `inputs` / `outputs` are device
  * pointers sized by the descriptors, and the work is enqueued on `stream` (a hipStream_t; NULL is
  * the null stream) without synchronising. Borrowed in place as `binding.prepareBorrowed` does
- * (src/executable/binding.zig:138-200). */
+ * (src/executable/binding.zig:138-200), which refuses a slice below the backend's minimum
+ * alignment: here 16 bytes (hipMalloc's pointers are 256-byte aligned); a misaligned pointer or a
+ * count that does not match returns ACCY_HIP_INVALID_BUFFER before anything is launched. */
 int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t n_inputs, void* const* outputs,
                            size_t n_outputs, void* stream);
 

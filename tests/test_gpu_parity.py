@@ -573,7 +573,16 @@ def test_executor_launches_many_times_and_device_invoke():
         assert ks[0].calls == 256 and ks[0].mean_ms > 0
         ex.set_profiling(False)
         assert_rel(dout.download(np.zeros(64, np.float32)), ref, 1e-5)
-        for b in (dx, dout):
+        # Device buffers are used in place with 16-byte accesses: a misaligned pointer is refused
+        # before anything is launched (binding.zig:138-200), and the output keeps its contents.
+        big = hip.DeviceBuffer(64 * 4 + 16)
+        for bad_in, bad_out in [(dx.ptr + 4, dout.ptr), (dx.ptr, big.ptr + 8)]:
+            with pytest.raises(hip.HipError) as e:
+                ex.launch_device([bad_in], [bad_out], stream.handle)
+            assert e.value.status == hip.INVALID_BUFFER
+        stream.synchronize()
+        assert_rel(dout.download(np.zeros(64, np.float32)), ref, 1e-5)
+        for b in (dx, dout, big):
             b.free()
         stream.destroy()
 

@@ -481,31 +481,22 @@ struct Accumulator {
   }
 };
 
-// Workgroup of 2 * C::WAVES waves (128 * C::WAVES threads) over 64 * C::WAVES queries of one batch
-// index.
+// Query blocks per workgroup: under a causal mask with an even number of query blocks, a workgroup
+// takes block NQB - 1 - p and then block p, so that every workgroup streams the same number of key
+// blocks (the heavy blocks start first); the grid is NB * NQB / blocks_per_group workgroups.
 template <class C>
-__device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
-                                      const u16_t* __restrict__ V, u16_t* __restrict__ O) {
-  constexpr int WAVES = C::WAVES, QT = 2;
-  constexpr long BQ = 64 * WAVES, NQB = C::SQ / BQ, NKB = C::SK / BK;
-  static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
-  __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
-  __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
-  __shared__ __attribute__((aligned(16))) u32x4 pbuf[2 * WAVES * QT * 2 * 64];
-  __shared__ __attribute__((aligned(16))) float abuf[2 * WAVES * 64 * QT];
-  __shared__ __attribute__((aligned(16))) float lbuf[WAVES * 64 * QT];
-  u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
-  u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
-  const Lds<C> sh{ks, vs, pbuf, abuf, lbuf};
+constexpr long blocks_per_group() {
+  constexpr long NQB = C::SQ / (64 * C::WAVES);
+  return C::CAUSAL && NQB % 2 == 0 ? 2 : 1;
+}
 
-  // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
-  // query blocks with the most keys start first.
-  const long total = (long)gridDim.x;
-  long t = (long)blockIdx.x;
-  if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
-  const long b = t / NQB;
-  long qb = t % NQB;
-  if constexpr (C::CAUSAL) qb = NQB - 1 - qb;
+// One query block (queries qb * 64 * WAVES ...) of batch index b, by the workgroup's scorer and
+// accumulator waves. Both roles meet nkb + 2 barriers, so blocks can follow each other.
+template <class C>
+__device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
+                                            const u16_t* __restrict__ V, u16_t* __restrict__ O, long b, long qb) {
+  constexpr int WAVES = C::WAVES;
+  constexpr long BQ = 64 * WAVES, NKB = C::SK / BK;
   const long q0 = qb * BQ;
   long nkb = NKB;
   if constexpr (C::CAUSAL) {
@@ -531,6 +522,39 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
     f.wave = w - WAVES;
     f.lane = lane;
     f.run(O, b, nkb);
+  }
+}
+
+// Workgroup of 2 * C::WAVES waves (128 * C::WAVES threads) over blocks_per_group<C>() query blocks
+// of 64 * C::WAVES queries of one batch index.
+template <class C>
+__device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
+                                      const u16_t* __restrict__ V, u16_t* __restrict__ O) {
+  constexpr int WAVES = C::WAVES, QT = 2;
+  constexpr long BQ = 64 * WAVES, NQB = C::SQ / BQ, PAIR = blocks_per_group<C>(), PER_B = NQB / PAIR;
+  static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
+  __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
+  __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
+  __shared__ __attribute__((aligned(16))) u32x4 pbuf[2 * WAVES * QT * 2 * 64];
+  __shared__ __attribute__((aligned(16))) float abuf[2 * WAVES * 64 * QT];
+  __shared__ __attribute__((aligned(16))) float lbuf[WAVES * 64 * QT];
+  u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
+  u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
+  const Lds<C> sh{ks, vs, pbuf, abuf, lbuf};
+
+  // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
+  // query blocks with the most keys start first.
+  const long total = (long)gridDim.x;
+  long t = (long)blockIdx.x;
+  if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+  const long b = t / PER_B, p = t % PER_B;
+  if (b >= C::NB) return;  // a grid larger than the work
+  if constexpr (PAIR == 2) {
+    flash_block<C>(sh, Q, K, V, O, b, NQB - 1 - p);
+    gemm::wait_vmcnt<0>();  // the first block's output stores, before the second block's waits
+    flash_block<C>(sh, Q, K, V, O, b, p);
+  } else {
+    flash_block<C>(sh, Q, K, V, O, b, C::CAUSAL ? NQB - 1 - p : p);
   }
 }
 

@@ -1169,7 +1169,11 @@ class Planner {
     KernelStep ks;
     ks.source = src.str();
     ks.name = nm;
-    ks.grid[0] = (uint32_t)(L.nb * (L.sq / (64 * waves)));
+    // Causal with an even number of query blocks: two complementary blocks per workgroup
+    // (attn::blocks_per_group), so every workgroup streams the same number of keys.
+    const int64_t nqb = L.sq / (64 * waves);
+    const int64_t pair = at.causal && nqb % 2 == 0 ? 2 : 1;
+    ks.grid[0] = (uint32_t)(L.nb * nqb / pair);
     ks.block[0] = 128 * waves;  // a scorer and an accumulator wave per 64 queries
     ks.klass = "attention";
     ks.label = "attention:%" + std::to_string(pv);

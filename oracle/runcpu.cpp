@@ -138,14 +138,27 @@ double unary_f64(Unary u, double x) {
   return x;
 }
 
+// Float max / min as the reference's x64 backend emits them
+// (deps/lib/compiler/choir/src/backends/x64/scalar.zig:675-720): maxss / minss, which return the
+// second operand on a tie and when either operand is NaN, then the first operand when that result is
+// NaN. NaN is thus skipped unless both are NaN, and a +0 / -0 tie gives the second operand.
+template <typename F> F ref_max(F a, F b) {
+  const F r = a > b ? a : b;
+  return r != r ? a : r;
+}
+template <typename F> F ref_min(F a, F b) {
+  const F r = a < b ? a : b;
+  return r != r ? a : r;
+}
+
 float binary_f32(Binary b, float x, float y) {
   switch (b) {
     case Binary::add: return x + y;
     case Binary::sub: return x - y;
     case Binary::mul: return x * y;
     case Binary::div: return x / y;
-    case Binary::max: return fmaxf(x, y);
-    case Binary::min: return fminf(x, y);
+    case Binary::max: return ref_max(x, y);
+    case Binary::min: return ref_min(x, y);
     case Binary::pow: return powf(x, y);
   }
   return x;
@@ -157,8 +170,8 @@ double binary_f64(Binary b, double x, double y) {
     case Binary::sub: return x - y;
     case Binary::mul: return x * y;
     case Binary::div: return x / y;
-    case Binary::max: return std::fmax(x, y);
-    case Binary::min: return std::fmin(x, y);
+    case Binary::max: return ref_max(x, y);
+    case Binary::min: return ref_min(x, y);
     case Binary::pow: return std::pow(x, y);
   }
   return x;
@@ -475,12 +488,12 @@ class Evaluator {
           const float* px = x.as<float>() + base;
           for (uint64_t r = 0; r < nred; ++r) {
             float val = px[roff[r]];
-            acc = rk == Reducer::sum ? acc + val : rk == Reducer::max ? fmaxf(acc, val) : fminf(acc, val);
+            acc = rk == Reducer::sum ? acc + val : rk == Reducer::max ? ref_max(acc, val) : ref_min(acc, val);
           }
         } else {
           for (uint64_t r = 0; r < nred; ++r) {
             float val = (float)load_f(x, base + roff[r]);
-            acc = rk == Reducer::sum ? acc + val : rk == Reducer::max ? fmaxf(acc, val) : fminf(acc, val);
+            acc = rk == Reducer::sum ? acc + val : rk == Reducer::max ? ref_max(acc, val) : ref_min(acc, val);
           }
         }
         store_f(t, o, acc);
@@ -488,7 +501,7 @@ class Evaluator {
         double acc = load_f(init, 0);
         for (uint64_t r = 0; r < nred; ++r) {
           double val = load_f(x, base + roff[r]);
-          acc = rk == Reducer::sum ? acc + val : rk == Reducer::max ? std::fmax(acc, val) : std::fmin(acc, val);
+          acc = rk == Reducer::sum ? acc + val : rk == Reducer::max ? ref_max(acc, val) : ref_min(acc, val);
         }
         store_f(t, o, acc);
       } else {

@@ -420,6 +420,58 @@ def test_device_tanh_against_float64():
     assert tail[3] == 0.0 and np.signbit(tail[3]) and tail[4] == 0.0 and not np.signbit(tail[4])
 
 
+@pytest.mark.parametrize("width", [16, 4096])
+def test_nan_and_infinity_propagate_as_in_runcpu(width):
+    """Sum, max, min and logsumexp over rows holding NaN and +-inf, on the serial fold (16 columns)
+    and on the row kernel (4096): max / min skip NaN unless every value is NaN (the reference's
+    maxss / minss with a NaN fix-up, x64/scalar.zig:661-720), sums propagate NaN, +inf - inf is NaN,
+    and logsumexp of a row whose maximum is +-inf is NaN (x - max). Rows avoid overflow patterns
+    whose result depends on the summation order."""
+    rng = np.random.default_rng(5)
+    base = rng.standard_normal((8, width)).astype(np.float32)
+    rows = []
+    for r in range(8):
+        x = base[r].copy()
+        if r == 1:
+            x[width // 3] = np.nan
+        elif r == 2:
+            x[:] = np.nan
+        elif r == 3:
+            x[width // 2] = np.inf
+        elif r == 4:
+            x[width // 2], x[width // 4] = np.inf, -np.inf
+        elif r == 5:
+            x[:] = -np.inf
+        elif r == 6:
+            x[0], x[-1] = np.nan, np.inf
+        rows.append(x)
+    x = np.stack(rows)
+    prog = T.define("special", [T.spec("f32", r=8, c=width)],
+                    lambda b, a: [a[0].sum("c"), a[0].max("c"), a[0].min("c")])
+    got = hip_run(prog, [x])
+    ref = oracle_run(prog, [x])
+    for g, r in zip(got, ref):
+        np.testing.assert_allclose(g, r, rtol=1e-5, equal_nan=True)
+    got = hip_run(W.logsumexp_program(8, width), [x])[0]
+    ref = oracle_run(W.logsumexp_program(8, width), [x])[0]
+    np.testing.assert_allclose(got, ref, rtol=1e-5, equal_nan=True)
+    assert np.isnan(got[[2, 3, 4, 5]]).all() and np.isfinite(got[[0, 7]]).all()
+
+
+def test_softmax_with_masked_entries_matches_oracle():
+    """Entries at -inf (a mask) get probability 0; a row that is -inf everywhere is NaN in both."""
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((4, 256)).astype(np.float32)
+    x[0, ::3] = -np.inf
+    x[1, :] = -np.inf
+    prog = T.define("sm", [T.spec("f32", r=4, c=256)],
+                    lambda b, a: (lambda e: e.div(e.sum("c")))(a[0].sub(a[0].max("c")).exp()))
+    got = hip_run(prog, [x])[0]
+    ref = oracle_run(prog, [x])[0]
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-7, equal_nan=True)
+    assert (got[0, ::3] == 0).all() and np.isnan(got[1]).all()
+
+
 def _ulp_error(got, ref):
     """|got - ref| in units of the f32 spacing at the float64 result."""
     spacing = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)

@@ -102,6 +102,30 @@ def test_max_and_min_reduce():
     assert np.array_equal(got[1], x.min(axis=0))
 
 
+def _maxss_rule(x, y, greater):
+    """deps/lib/compiler/choir/src/backends/x64/scalar.zig:675-720: maxss / minss return the second
+    operand on a tie or a NaN, then a NaN result is replaced by the first operand."""
+    r = x if ((x > y) if greater else (x < y)) else y
+    return x if np.isnan(r) else r
+
+
+def test_float_max_min_follow_maxss_with_nan_fixup():
+    a = np.array([np.nan, 1.0, np.nan, 0.0, -0.0, 2.0, -np.inf, 3.0], np.float32)
+    b = np.array([1.0, np.nan, np.nan, -0.0, 0.0, 2.0, np.inf, -3.0], np.float32)
+    prog = T.define("mm", [T.spec("f32", i=8), T.spec("f32", i=8)],
+                    lambda bb, v: [v[0].max(v[1]), v[0].min(v[1])])
+    mx, mn = oracle_run(prog, [a, b])
+    for i in range(8):
+        for got, greater in ((mx[i], True), (mn[i], False)):
+            want = np.float32(_maxss_rule(a[i], b[i], greater))
+            assert got.view(np.uint32) == want.view(np.uint32) or (np.isnan(got) and np.isnan(want)), (i, got, want)
+    # As a fold from -inf, a +0 / -0 tie keeps the later element's sign; NaN is skipped.
+    fold = T.define("f", [T.spec("f32", r=3, i=3)], lambda bb, v: v[0].max("i"))
+    x = np.array([[0.0, -0.0, -1.0], [-0.0, 0.0, -1.0], [np.nan, -5.0, np.nan]], np.float32)
+    got = oracle_run(fold, [x])[0]
+    assert np.signbit(got[0]) and not np.signbit(got[1]) and got[0] == 0 and got[2] == -5.0
+
+
 def test_f16_sum_widens_to_f32_and_rounds_once():
     # 4096 ones in f16: an f16 accumulator sticks at 2048; the f32 accumulator reaches 4096.
     x = np.ones(4096, np.float16)

@@ -296,6 +296,30 @@ int accy_hip_kernel_info(accy_hip_handle h, size_t index, accy_hip_kernel_stats*
   return ACCY_HIP_OK;
 }
 
+// Writes each step of a plan; a loop step's body plan follows, indented by its nesting depth.
+static void append_plan_source(const Plan& plan, bool compile, const std::string& indent, std::string& text) {
+  for (const Step& st : plan.steps) {
+    if (st.type == Step::Copy) {
+      text += indent + "// copy slot " + std::to_string(st.copy.src) + " -> " + std::to_string(st.copy.dst) + "\n";
+      continue;
+    }
+    if (st.type == Step::Loop) {
+      text += indent + "// loop " + std::to_string(st.loop.length) + " times over " +
+              std::to_string(st.loop.init_slots.size()) + " carries {\n";
+      append_plan_source(*st.loop.plan, compile, indent + "  ", text);
+      text += indent + "// }\n";
+      continue;
+    }
+    const KernelStep& k = st.kernel;
+    text += indent + "// " + k.label + " grid " + std::to_string(k.grid[0]) + " block " + std::to_string(k.block[0]) + "\n";
+    if (k.candidate_count > 1)
+      text += indent + "// tuning " + k.tuning_key + " candidate " + std::to_string(k.candidate) + " of " +
+              std::to_string(k.candidate_count) + "\n";
+    text += k.source;
+    if (compile) compile_kernel_source(full_kernel_source(k.source), k.name);
+  }
+}
+
 int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile, char* buf, size_t cap,
                          size_t* needed) {
   return guarded([&]() -> int {
@@ -310,19 +334,7 @@ int accy_hip_plan_source(const uint8_t* wire_bytes, size_t wire_len, int compile
     opt.tuning = &process_tuning();
     Plan plan = lower(prog, opt);
     std::string text;
-    for (const Step& st : plan.steps) {
-      if (st.type == Step::Copy) {
-        text += "// copy slot " + std::to_string(st.copy.src) + " -> " + std::to_string(st.copy.dst) + "\n";
-        continue;
-      }
-      const KernelStep& k = st.kernel;
-      text += "// " + k.label + " grid " + std::to_string(k.grid[0]) + " block " + std::to_string(k.block[0]) + "\n";
-      if (k.candidate_count > 1)
-        text += "// tuning " + k.tuning_key + " candidate " + std::to_string(k.candidate) + " of " +
-                std::to_string(k.candidate_count) + "\n";
-      text += k.source;
-      if (compile) compile_kernel_source(full_kernel_source(k.source), k.name);
-    }
+    append_plan_source(plan, compile != 0, "", text);
     if (needed) *needed = text.size() + 1;
     if (buf && cap) {
       size_t n = std::min(cap - 1, text.size());

@@ -9,6 +9,7 @@
 
 #include <cstdint>
 #include <map>
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -51,10 +52,23 @@ struct CopyStep {
   uint64_t bytes = 0;
 };
 
+struct Plan;
+
+// A scan run as a host loop (src/tensor/lower.zig:119-167 lowers scans unrolled or host-looped): the
+// body's plan runs `length` times, its parameters the current carries and its outputs the next ones.
+struct LoopStep {
+  std::shared_ptr<const Graph> body;
+  std::shared_ptr<const Plan> plan;  // the body's plan (input / output slots = carries in / out)
+  int64_t length = 0;
+  std::vector<int> init_slots;       // per carry: the slot of its initial value
+  std::vector<int> result_slots;     // per carry: the slot that receives its final value, or -1
+};
+
 struct Step {
-  enum Type : uint8_t { Kernel, Copy } type = Kernel;
+  enum Type : uint8_t { Kernel, Copy, Loop } type = Kernel;
   KernelStep kernel;
   CopyStep copy;
+  LoopStep loop;
 };
 
 struct Plan {

@@ -155,7 +155,9 @@ class Planner {
         break;
       case Kind::dot_general: dot(v); break;
       case Kind::scatter_add: scatter_add(v); break;
-      case Kind::scan: case Kind::projection: case Kind::custom_call: case Kind::sparse_cross_entropy:
+      case Kind::scan: scan(v); break;
+      case Kind::projection: break;  // written by its scan's loop step
+      case Kind::custom_call: case Kind::sparse_cross_entropy:
         fail(Err::Unsupported, std::string(kind_name(op.kind)) + " is not supported by the HIP target");
       default:
         if (needed_[v]) map(v);
@@ -200,6 +202,64 @@ class Planner {
   void finish(uint32_t v) {
     done_[v] = true;
     slots_.produced[v] = true;
+  }
+
+  // Slot of value a, materialised by a map kernel when so far it is only evaluated inline.
+  int materialize(uint32_t a) {
+    int s = slots_.available(a);
+    if (s >= 0) return s;
+    if (!is_inlinable(g_.ops[a].kind)) fail(Err::Unsupported, "value not computed before its use");
+    map(a);
+    return slots_.available(a);
+  }
+
+  // ---- scan: the body's own plan, run as a host loop over two sets of carry buffers ----
+  // The scan's value is carry 0 and projection i is carry i (builder.zig:899-990); a carry without a
+  // reader gets no result slot.
+  void scan(uint32_t v) {
+    const Op& op = g_.ops[v];
+    Step st;
+    st.type = Step::Loop;
+    LoopStep& L = st.loop;
+    L.body = op.body;
+    LowerOptions bo = opt_;
+    bo.force_candidate.clear();
+    L.plan = std::make_shared<const Plan>(lower(*op.body, bo));
+    L.length = op.axis;
+    for (uint32_t a : op.args) L.init_slots.push_back(materialize(a));
+    L.result_slots.assign(op.args.size(), -1);
+    std::vector<CopyStep> extra;  // a second projection of a carry that is also a program output
+    auto take = [&](uint32_t value, size_t carry) {
+      if (L.result_slots[carry] >= 0 && slots_.slot_of[value] < 0) {
+        slots_.slot_of[value] = L.result_slots[carry];  // another projection of the same carry: same slot
+        finish(value);
+        return;
+      }
+      const int s = slots_.slot_of[value] >= 0 ? slots_.slot_of[value] : temp_slot(value);
+      if (L.result_slots[carry] < 0) {
+        L.result_slots[carry] = s;
+      } else {
+        CopyStep c;
+        c.src = L.result_slots[carry];
+        c.dst = s;
+        c.bytes = g_.type(value).bytes();
+        extra.push_back(c);
+      }
+      finish(value);
+    };
+    take(v, 0);
+    for (uint32_t u = v + 1; u < (uint32_t)g_.ops.size(); ++u) {
+      const Op& p = g_.ops[u];
+      if (p.kind == Kind::projection && p.args[0] == v && live_[u]) take(u, (size_t)p.index);
+    }
+    plan_.steps.push_back(std::move(st));
+    for (const CopyStep& c : extra) {
+      if (!c.bytes) continue;
+      Step cs;
+      cs.type = Step::Copy;
+      cs.copy = c;
+      plan_.steps.push_back(cs);
+    }
   }
 
   // ---- map: out[i] = value at i ----

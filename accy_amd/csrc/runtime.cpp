@@ -127,6 +127,22 @@ Executor::Executor(Program program, Plan plan) : program_(std::move(program)), p
         check(hipMemcpy(owned_[i], s.data.data(), s.bytes, hipMemcpyHostToDevice), "hipMemcpy");
     }
     fn_.assign(plan_.steps.size(), nullptr);
+    loops_.resize(plan_.steps.size());
+    loop_bufs_.resize(plan_.steps.size());
+    for (size_t i = 0; i < plan_.steps.size(); ++i) {
+      const Step& st = plan_.steps[i];
+      if (st.type != Step::Loop) continue;
+      const Plan& bp = *st.loop.plan;
+      loops_[i] = std::make_unique<Executor>(*st.loop.body, bp);
+      const size_t nc = bp.input_slots.size();
+      loop_bufs_[i].assign(2 * nc, nullptr);
+      for (size_t c = 0; c < nc; ++c) {
+        const uint64_t bytes = bp.slots[(size_t)bp.input_slots[c]].bytes;
+        if (!bytes) continue;
+        check(hipMalloc(&loop_bufs_[i][c], bytes), "hipMalloc");
+        check(hipMalloc(&loop_bufs_[i][nc + c], bytes), "hipMalloc");
+      }
+    }
     int dev = 0, max_lds = 0;
     check(hipGetDevice(&dev), "hipGetDevice");
     check(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
@@ -147,6 +163,9 @@ Executor::Executor(Program program, Plan plan) : program_(std::move(program)), p
   } catch (...) {
     for (void* p : owned_)
       if (p) (void)hipFree(p);
+    for (auto& bufs : loop_bufs_)
+      for (void* p : bufs)
+        if (p) (void)hipFree(p);
     if (stream_) (void)hipStreamDestroy(stream_);
     throw;
   }
@@ -157,7 +176,40 @@ Executor::~Executor() {
   for (hipEvent_t e : events_) (void)hipEventDestroy(e);
   for (void* p : owned_)
     if (p) (void)hipFree(p);
+  for (auto& bufs : loop_bufs_)
+    for (void* p : bufs)
+      if (p) (void)hipFree(p);
   if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+// Carries start as copies of the initial values; each iteration runs the body from one buffer set
+// into the other on the same stream; the final carries are copied to the slots that read them.
+void Executor::run_loop(size_t step, hipStream_t stream) {
+  const LoopStep& L = plan_.steps[step].loop;
+  const Plan& bp = *L.plan;
+  const size_t nc = bp.input_slots.size();
+  std::vector<void*>& buf = loop_bufs_[step];
+  auto bytes = [&](size_t c) { return bp.slots[(size_t)bp.input_slots[c]].bytes; };
+  for (size_t c = 0; c < nc; ++c)
+    if (bytes(c))
+      check(hipMemcpyAsync(buf[c], bound_[(size_t)L.init_slots[c]], bytes(c), hipMemcpyDeviceToDevice, stream),
+            "hipMemcpyAsync");
+  size_t cur = 0;
+  std::vector<const void*> in(nc);
+  std::vector<void*> out(nc);
+  for (int64_t it = 0; it < L.length; ++it) {
+    for (size_t c = 0; c < nc; ++c) {
+      in[c] = buf[cur * nc + c];
+      out[c] = buf[(1 - cur) * nc + c];
+    }
+    loops_[step]->invoke_device(in.data(), nc, out.data(), nc, stream);
+    cur = 1 - cur;
+  }
+  for (size_t c = 0; c < nc; ++c)
+    if (L.result_slots[c] >= 0 && bytes(c))
+      check(hipMemcpyAsync(bound_[(size_t)L.result_slots[c]], buf[cur * nc + c], bytes(c), hipMemcpyDeviceToDevice,
+                           stream),
+            "hipMemcpyAsync");
 }
 
 void Executor::set_profiling(bool on) {
@@ -211,6 +263,10 @@ void Executor::run_steps(hipStream_t stream) {
       check(hipMemcpyAsync(bound_[(size_t)st.copy.dst], bound_[(size_t)st.copy.src], st.copy.bytes,
                            hipMemcpyDeviceToDevice, stream),
             "hipMemcpyAsync");
+      continue;
+    }
+    if (st.type == Step::Loop) {
+      run_loop(i, stream);
       continue;
     }
     const KernelStep& k = st.kernel;

@@ -81,6 +81,10 @@ class Executor {
   size_t recorded_ = 0;            // invocations recorded since profiling was turned on
   std::vector<hipEvent_t> events_;  // kProfiledCalls slots of 2 events per kernel
   std::vector<KernelTiming> timings_;
+  // Loop steps: the body's executor and two sets of carry buffers (carries in / out), per step.
+  std::vector<std::unique_ptr<Executor>> loops_;
+  std::vector<std::vector<void*>> loop_bufs_;
+  void run_loop(size_t step, hipStream_t stream);
 };
 
 int device_count();

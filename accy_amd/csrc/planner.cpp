@@ -157,7 +157,7 @@ class Planner {
       case Kind::scatter_add: scatter_add(v); break;
       case Kind::scan: scan(v); break;
       case Kind::projection: break;  // written by its scan's loop step
-      case Kind::custom_call: case Kind::sparse_cross_entropy:
+      case Kind::custom_call: case Kind::sparse_cross_entropy:  // sparse_cross_entropy is expanded before planning
         fail(Err::Unsupported, std::string(kind_name(op.kind)) + " is not supported by the HIP target");
       default:
         if (needed_[v]) map(v);
@@ -1740,8 +1740,91 @@ class Planner {
   }
 };
 
+// Lowest finite value of a float dtype as its storage bytes (`lowerFloatLowestConstant`,
+// src/tensor/lower.zig:1005-1029): f16 -65504, bf16 the truncated -floatMax(f32), f32 / f64 -floatMax.
+std::string lowest_finite_bytes(DType dt) {
+  std::string b(dtype_size(dt), '\0');
+  switch (dt) {
+    case DType::f16: { const uint16_t h = 0xFBFF; std::memcpy(&b[0], &h, 2); break; }
+    case DType::bf16: { const uint16_t h = f32_to_bf16_trunc(-3.40282347e+38f); std::memcpy(&b[0], &h, 2); break; }
+    case DType::f32: { const float f = -3.40282347e+38f; std::memcpy(&b[0], &f, 4); break; }
+    case DType::f64: { const double d = -1.7976931348623157e+308; std::memcpy(&b[0], &d, 8); break; }
+    default: fail(Err::Unsupported, "sparse_cross_entropy on a non-float dtype");
+  }
+  return b;
+}
+
+// sparse_cross_entropy in the expanded form runCpu lowers it to (no kernel library;
+// `lowerSparseCrossEntropyExpanded`, src/tensor/lower.zig:914-1003), with m the row max from the
+// lowest finite value, over the class axis:
+//   loss = log(sum(exp(x - m))) - sum(select(iota == target, x - m, 0)).
+// The planner then fuses the three row reductions like any other (one row kernel per loss).
+Graph expand_sparse_cross_entropy(const Graph& g) {
+  Graph out;
+  out.name = g.name;
+  std::vector<uint32_t> id(g.ops.size());
+  auto push = [&](Op op) {
+    out.ops.push_back(std::move(op));
+    return (uint32_t)(out.ops.size() - 1);
+  };
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    const Op& src = g.ops[i];
+    if (src.kind != Kind::sparse_cross_entropy) {
+      Op op = src;
+      for (uint32_t& a : op.args) a = id[a];
+      id[i] = push(std::move(op));
+      continue;
+    }
+    const uint32_t x = id[src.args[0]], t = id[src.args[1]];
+    const Type lt = out.ops[x].result;  // a copy: push() below grows out.ops
+    const int64_t axis = src.axis;
+    std::vector<int64_t> keep;  // positions of the non-class axes
+    for (int64_t d = 0; d < (int64_t)lt.rank(); ++d)
+      if (d != axis) keep.push_back(d);
+    const Type scalar{lt.dtype, {}}, row = src.result, idx{DType::i32, lt.dims}, mask{DType::i1, lt.dims};
+    auto constant = [&](std::string bytes) {
+      Op c; c.kind = Kind::constant; c.result = scalar; c.bytes = std::move(bytes);
+      return push(std::move(c));
+    };
+    auto reduce = [&](uint32_t a, uint32_t init, Reducer r) {
+      Op o; o.kind = Kind::reduce; o.code = (uint8_t)r; o.result = row; o.args = {a, init}; o.ints = {axis};
+      return push(std::move(o));
+    };
+    auto expand = [&](uint32_t a, const Type& to, std::vector<int64_t> dims) {
+      Op o; o.kind = Kind::broadcast_in_dim; o.result = to; o.args = {a}; o.ints = std::move(dims);
+      return push(std::move(o));
+    };
+    auto elementwise = [&](Kind k, uint8_t code, const Type& to, std::vector<uint32_t> args) {
+      Op o; o.kind = k; o.code = code; o.result = to; o.args = std::move(args);
+      return push(std::move(o));
+    };
+    const uint32_t lowest = constant(lowest_finite_bytes(lt.dtype));
+    const uint32_t zero = constant(std::string(dtype_size(lt.dtype), '\0'));
+    const uint32_t m = reduce(x, lowest, Reducer::max);
+    const uint32_t shifted = elementwise(Kind::binary, (uint8_t)Binary::sub, lt, {x, expand(m, lt, keep)});
+    const uint32_t e = elementwise(Kind::unary, (uint8_t)Unary::exp, lt, {shifted});
+    const uint32_t log_denominator = elementwise(Kind::unary, (uint8_t)Unary::log, row, {reduce(e, zero, Reducer::sum)});
+    Op io; io.kind = Kind::iota; io.result = idx; io.axis = axis;
+    const uint32_t positions = push(std::move(io));
+    const uint32_t hit = elementwise(Kind::compare, (uint8_t)Cmp::eq, mask, {positions, expand(t, idx, keep)});
+    const uint32_t selected = elementwise(Kind::select, 0, lt, {hit, shifted, expand(zero, lt, {})});
+    const uint32_t picked = reduce(selected, zero, Reducer::sum);
+    id[i] = elementwise(Kind::binary, (uint8_t)Binary::sub, row, {log_denominator, picked});
+  }
+  for (uint32_t p : g.params) out.params.push_back(id[p]);
+  for (uint32_t o : g.outputs) out.outputs.push_back(id[o]);
+  return out;
+}
+
 }  // namespace
 
-Plan lower(const Program& program, const LowerOptions& options) { return Planner(program, options).run(); }
+Plan lower(const Program& program, const LowerOptions& options) {
+  for (const Op& op : program.ops)
+    if (op.kind == Kind::sparse_cross_entropy) {
+      const Graph expanded = expand_sparse_cross_entropy(program);
+      return Planner(expanded, options).run();
+    }
+  return Planner(program, options).run();
+}
 
 }  // namespace accy

@@ -25,6 +25,7 @@
 #include <cstdint>
 #include <cstring>
 #include <functional>
+#include <limits>
 #include <map>
 #include <string>
 #include <vector>
@@ -328,14 +329,54 @@ class Evaluator {
         const Op& src = g_.ops[op.args[0]];
         return scans_.at(&src).at(op.index);
       }
-      case Kind::sparse_cross_entropy:
-        fail(Err::Unsupported, "sparse_cross_entropy is not restated by the oracle");
+      case Kind::sparse_cross_entropy: return sparse_cross_entropy(op, v[op.args[0]], v[op.args[1]]);
       case Kind::custom_call: fail(Err::Unsupported, "custom_call " + op.bytes);
     }
     fail(Err::Unsupported);
   }
 
   std::map<const Op*, std::vector<Tensor>> scans_;
+
+  // runCpu takes the expanded form (src/tensor/lower.zig:914-1003; no kernel library is configured,
+  // lower.zig:178-182): the op sequence is rebuilt here with the checked builder and evaluated with
+  // this file's own reduce / elementwise rules. m starts from the lowest finite value
+  // (lower.zig:1005-1029), so a row of -inf keeps m finite.
+  Tensor sparse_cross_entropy(const Op& op, const Tensor& logits, const Tensor& targets) {
+    const Type& lt = logits.type;
+    const DType dt = lt.dtype;
+    std::string lowest(dtype_size(dt), '\0');
+    if (dt == DType::f16) {
+      const uint16_t h = f32_to_f16_bits(-65504.0f);
+      std::memcpy(&lowest[0], &h, 2);
+    } else if (dt == DType::bf16) {
+      const uint16_t h = f32_to_bf16_trunc(-std::numeric_limits<float>::max());
+      std::memcpy(&lowest[0], &h, 2);
+    } else if (dt == DType::f32) {
+      const float f = -std::numeric_limits<float>::max();
+      std::memcpy(&lowest[0], &f, 4);
+    } else {
+      const double d = -std::numeric_limits<double>::max();
+      std::memcpy(&lowest[0], &d, 8);
+    }
+    Builder b("sparse_cross_entropy");
+    const uint32_t x = b.input(lt), t = b.input(targets.type);
+    std::vector<int64_t> rest;
+    for (int64_t d = 0; d < (int64_t)lt.rank(); ++d)
+      if (d != op.axis) rest.push_back(d);
+    const uint32_t lo = b.constant(Type{dt, {}}, lowest);
+    const uint32_t zero = b.constant(Type{dt, {}}, std::string(dtype_size(dt), '\0'));
+    const uint32_t row_max = b.reduce(x, lo, Reducer::max, {op.axis});
+    const uint32_t shifted = b.binary(Binary::sub, x, b.broadcast_in_dim(row_max, lt.dims, rest));
+    const uint32_t denominator = b.reduce(b.unary(Unary::exp, shifted), zero, Reducer::sum, {op.axis});
+    const uint32_t positions = b.iota(Type{DType::i32, lt.dims}, op.axis);
+    const uint32_t wanted = b.broadcast_in_dim(t, lt.dims, rest);
+    const uint32_t on_target = b.compare(Cmp::eq, positions, wanted);
+    const uint32_t kept = b.select(on_target, shifted, b.broadcast_in_dim(zero, lt.dims, {}));
+    const uint32_t target_shifted = b.reduce(kept, zero, Reducer::sum, {op.axis});
+    const uint32_t loss = b.binary(Binary::sub, b.unary(Unary::log, denominator), target_shifted);
+    const Graph g = b.finish({loss});
+    return Evaluator(g).run({logits, targets})[0];
+  }
 
   Tensor unary(const Op& op, const Tensor& a) {
     Tensor t = make(op.result);

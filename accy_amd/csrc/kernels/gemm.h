@@ -366,20 +366,23 @@ struct Frags {
   }
 };
 
-// One K step on stage STAGE. On entry f0 holds this step's first sub-step fragments and every wave
-// has finished reading the previous stage (NEXT). The first half runs the MFMAs of f0 with the
-// loads of tile kt + 3 into NEXT and the reads of this stage's second sub-step (f1) slotted between
-// them; then the wave waits for its own loads of tile kt + 1 and its LDS reads and meets the other
-// waves at the step's single barrier (after which tile kt + 1 is complete and nobody reads this
-// stage any more); the second half runs the MFMAs of f1 with the reads of tile kt + 1's first
-// sub-step (the next f0) between them. The explicit interleave keeps at most one sub-step of LDS
-// reads in flight, so the compiler's lgkmcnt waits stay exact instead of draining the counter.
-template <class C, int STAGE, int NEXT, int WAIT, bool ISSUE, bool HAS_NEXT>
+// One K step on stage STAGE of S = C::STAGES. On entry f0 holds this step's first sub-step fragments
+// and every wave has finished reading the previous stage (NEXT). The first half runs the MFMAs of f0
+// with the loads of tile kt + S - 1 into NEXT and the reads of this stage's second sub-step (f1)
+// slotted between them; then the wave waits for its own loads of tile kt + 1 (WAIT = the load
+// instructions it may leave in flight) and its LDS reads and meets the other waves at the step's
+// single barrier (after which tile kt + 1 is complete and nobody reads this stage any more); the
+// second half runs the MFMAs of f1 with the reads of tile kt + 1's first sub-step (the next f0)
+// between them. The explicit interleave keeps at most one sub-step of LDS reads in flight, so the
+// compiler's lgkmcnt waits stay exact instead of draining the counter.
+template <class C, int STAGE, int WAIT, bool ISSUE, bool HAS_NEXT>
 struct DmaStep {
+  static constexpr int S = C::STAGES, NEXT = (STAGE + S - 1) % S;
   template <class Acc>
   __device__ __forceinline__ static void run(const u16_t* __restrict__ Ab, const u16_t* __restrict__ Bb, long m0,
-                                             long n0, long kt, u16_t* const (&as)[4], u16_t* const (&bs)[4],
-                                             Frags<C>& f0, Acc& acc, int wave, int lane, int wm, int wn) {
+                                             long n0, long kt, u16_t* const (&as)[C::STAGES],
+                                             u16_t* const (&bs)[C::STAGES], Frags<C>& f0, Acc& acc, int wave, int lane,
+                                             int wm, int wn) {
     constexpr int NM = Frags<C>::TM * Frags<C>::TN, NF = Frags<C>::COUNT;
     constexpr int DA = C::BM * 64 / 1024 / 4, DB = C::BN * 64 / 1024 / 4;
     constexpr int ND = ISSUE ? DA + DB : 0, NI = NF + ND;
@@ -394,9 +397,9 @@ struct DmaStep {
         if (k < NF) {
           f1.load_one(k, as[STAGE], bs[STAGE], 1, lane, wm, wn);
         } else if (k - NF < DA) {
-          dma_part<C::BM, C::A_KC, AOff<C>>(Ab, m0, (kt + 3) * 32, as[NEXT], wave, lane, k - NF);
+          dma_part<C::BM, C::A_KC, AOff<C>>(Ab, m0, (kt + S - 1) * 32, as[NEXT], wave, lane, k - NF);
         } else {
-          dma_part<C::BN, C::B_KC, BOff<C>>(Bb, n0, (kt + 3) * 32, bs[NEXT], wave, lane, k - NF - DA);
+          dma_part<C::BN, C::B_KC, BOff<C>>(Bb, n0, (kt + S - 1) * 32, bs[NEXT], wave, lane, k - NF - DA);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -413,25 +416,72 @@ struct DmaStep {
       // before the next step's first MFMA.
       if constexpr (HAS_NEXT) {
         static_assert(NF <= NM, "fragment reads fit one per MFMA");
-        if (t < NF) f0.load_one(t, as[(STAGE + 1) & 3], bs[(STAGE + 1) & 3], 0, lane, wm, wn);
+        if (t < NF) f0.load_one(t, as[(STAGE + 1) % S], bs[(STAGE + 1) % S], 0, lane, wm, wn);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 };
 
-// Requires M % BM == 0, N % BN == 0, K % 128 == 0, 16-byte aligned rows; 256 threads (2 x 2 waves).
+// Steps after the last full group of S: R more steps that issue a load (the last of them issues tile
+// KT - 1), then S - 1 steps that only drain the pipeline (step j of those may leave S - 2 - j tiles in
+// flight; the last has no next tile). Step I of this tail runs on stage I % S.
+template <class C, int I, int R, int PER>
+struct DmaTail {
+  static constexpr int S = C::STAGES;
+  template <class Acc>
+  __device__ __forceinline__ static void run(const u16_t* __restrict__ Ab, const u16_t* __restrict__ Bb, long m0,
+                                             long n0, long kt, u16_t* const (&as)[S], u16_t* const (&bs)[S],
+                                             Frags<C>& f0, Acc& acc, int wave, int lane, int wm, int wn) {
+    constexpr bool ISSUE = I < R;
+    constexpr int J = ISSUE ? 0 : I - R + 1;  // 1 .. S - 1 for the draining steps
+    constexpr int LEFT = S - 2 - J;
+    constexpr int WAIT = LEFT > 0 ? LEFT * PER : 0;
+    constexpr bool HAS_NEXT = J < S - 1;
+    DmaStep<C, I % S, WAIT, ISSUE, HAS_NEXT>::run(Ab, Bb, m0, n0, kt, as, bs, f0, acc, wave, lane, wm, wn);
+    if constexpr (HAS_NEXT) DmaTail<C, I + 1, R, PER>::run(Ab, Bb, m0, n0, kt + 1, as, bs, f0, acc, wave, lane, wm, wn);
+  }
+};
+
+// One full group of S steps (stages 0 .. S - 1), each issuing a load.
+template <class C, int I, int PER>
+struct DmaGroup {
+  template <class Acc>
+  __device__ __forceinline__ static void run(const u16_t* __restrict__ Ab, const u16_t* __restrict__ Bb, long m0,
+                                             long n0, long kt, u16_t* const (&as)[C::STAGES],
+                                             u16_t* const (&bs)[C::STAGES], Frags<C>& f0, Acc& acc, int wave, int lane,
+                                             int wm, int wn) {
+    DmaStep<C, I, (C::STAGES - 2) * PER, true, true>::run(Ab, Bb, m0, n0, kt + I, as, bs, f0, acc, wave, lane, wm, wn);
+    if constexpr (I + 1 < C::STAGES) DmaGroup<C, I + 1, PER>::run(Ab, Bb, m0, n0, kt, as, bs, f0, acc, wave, lane, wm, wn);
+  }
+};
+
+// Requires M % BM == 0, N % BN == 0, K % 32 == 0 with at least STAGES K steps, 16-byte aligned rows;
+// 256 threads (2 x 2 waves). LDS: STAGES x (BM + BN) x 64 bytes (STAGES = 4 with a 256 x 256 tile:
+// 128 KiB, one workgroup per CU; 3 with 256 x 128: 72 KiB, two per CU when the kernel is compiled for
+// two waves per SIMD, so that one workgroup's epilogue runs beside the other's matrix work).
 template <class C, class Epi>
 __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi) {
-  constexpr int BM = C::BM, BN = C::BN;
+  constexpr int BM = C::BM, BN = C::BN, S = C::STAGES;
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr long TILES_M = C::M / BM, TILES_N = C::N / BN, KT = C::K / 32;
-  static_assert(C::M % BM == 0 && C::N % BN == 0 && C::K % 128 == 0, "exact tiles only");
+  static_assert(C::M % BM == 0 && C::N % BN == 0 && C::K % 32 == 0, "exact tiles only");
+  static_assert(S >= 2 && S <= 4 && KT >= S, "two to four stages, at least one K step per stage");
   constexpr int PER = (BM * 64 / 1024) / 4 + (BN * 64 / 1024) / 4;  // DMA instructions per wave per step
-  __shared__ __attribute__((aligned(1024))) u16_t a0[BM * 32], a1[BM * 32], a2[BM * 32], a3[BM * 32];
-  __shared__ __attribute__((aligned(1024))) u16_t b0[BN * 32], b1[BN * 32], b2[BN * 32], b3[BN * 32];
-  u16_t* const as[4] = {a0, a1, a2, a3};
-  u16_t* const bs[4] = {b0, b1, b2, b3};
+  static_assert((S - 2) * PER < 64, "vmcnt range");
+  // One LDS array per stage: with distinct objects the compiler can tell that the fragment reads of
+  // one stage do not overlap the direct-to-LDS writes still in flight into another (stages of one
+  // array would make it drain every load, s_waitcnt vmcnt(0), before each read). Stages past S get
+  // one element.
+  constexpr int A_ST = BM * 32, B_ST = BN * 32;
+  __shared__ __attribute__((aligned(1024))) u16_t a0[A_ST], a1[A_ST], a2[S > 2 ? A_ST : 1], a3[S > 3 ? A_ST : 1];
+  __shared__ __attribute__((aligned(1024))) u16_t b0[B_ST], b1[B_ST], b2[S > 2 ? B_ST : 1], b3[S > 3 ? B_ST : 1];
+  u16_t* const a_all[4] = {a0, a1, a2, a3};
+  u16_t* const b_all[4] = {b0, b1, b2, b3};
+  u16_t* const (&asc)[S] = *reinterpret_cast<u16_t* const(*)[S]>(&a_all);
+  u16_t* const (&bsc)[S] = *reinterpret_cast<u16_t* const(*)[S]>(&b_all);
+  u16_t* const (&as)[S] = asc;
+  u16_t* const (&bs)[S] = bsc;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
@@ -448,29 +498,23 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
     for (int j = 0; j < TN; ++j) acc[i][j] = f32x16{};
 
 #pragma unroll
-  for (int s = 0; s < 3; ++s) {
+  for (int s = 0; s < S - 1; ++s) {
     dma_tile<BM, C::A_KC, AOff<C>>(Ab, m0, s * 32, as[s], wave, lane);
     dma_tile<BN, C::B_KC, BOff<C>>(Bb, n0, s * 32, bs[s], wave, lane);
   }
-  // Tile 0 complete everywhere (tiles 1 and 2 may still be in flight), then its first sub-step.
+  // Tile 0 complete everywhere (tiles 1 .. S - 2 may still be in flight), then its first sub-step.
   Frags<C> f0;
-  wait_vmcnt<2 * PER>();
+  wait_vmcnt<(S - 2) * PER>();
   lds_reads_done_barrier();
 #pragma unroll
   for (int q = 0; q < Frags<C>::COUNT; ++q) f0.load_one(q, as[0], bs[0], 0, lane, wm, wn);
-  // Step kt issues tile kt + 3 and then waits for tile kt + 1: tiles kt + 2 and kt + 3 stay in flight.
+  // Step kt issues tile kt + S - 1 and then waits for tile kt + 1. Steps 0 .. KT - S issue a load:
+  // G full groups of S, then the tail.
+  constexpr long ISSUING = KT - S + 1, G = ISSUING / S;
+  constexpr int R = (int)(ISSUING % S);
   long kt = 0;
-  for (; kt + 4 < KT; kt += 4) {
-    DmaStep<C, 0, 3, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt, as, bs, f0, acc, wave, lane, wm, wn);
-    DmaStep<C, 1, 0, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt + 1, as, bs, f0, acc, wave, lane, wm, wn);
-    DmaStep<C, 2, 1, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt + 2, as, bs, f0, acc, wave, lane, wm, wn);
-    DmaStep<C, 3, 2, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt + 3, as, bs, f0, acc, wave, lane, wm, wn);
-  }
-  // Last four steps: only the first issues a load (tile KT - 1); the waits drain the pipeline.
-  DmaStep<C, 0, 3, 2 * PER, true, true>::run(Ab, Bb, m0, n0, kt, as, bs, f0, acc, wave, lane, wm, wn);
-  DmaStep<C, 1, 0, PER, false, true>::run(Ab, Bb, m0, n0, kt + 1, as, bs, f0, acc, wave, lane, wm, wn);
-  DmaStep<C, 2, 1, 0, false, true>::run(Ab, Bb, m0, n0, kt + 2, as, bs, f0, acc, wave, lane, wm, wn);
-  DmaStep<C, 3, 2, 0, false, false>::run(Ab, Bb, m0, n0, kt + 3, as, bs, f0, acc, wave, lane, wm, wn);
+  for (long g = 0; g < G; ++g, kt += S) DmaGroup<C, 0, PER>::run(Ab, Bb, m0, n0, kt, asc, bsc, f0, acc, wave, lane, wm, wn);
+  DmaTail<C, 0, R, PER>::run(Ab, Bb, m0, n0, kt, asc, bsc, f0, acc, wave, lane, wm, wn);
 
   const long col_base = n0 + wn * (BN / 2) + (lane & 31);
   const long row_base = m0 + wm * (BM / 2) + (lane >> 5) * 4;

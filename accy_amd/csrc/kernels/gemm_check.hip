@@ -46,7 +46,14 @@ struct CheckDmaNN : accy::gemm::Strided<0, 8192, 1, 0, 8192, 1> {
   static constexpr long M = 8192, N = 8192, K = 8192;
   static constexpr long A_B = 0, A_M = 8192, A_K = 1, B_B = 0, B_K = 8192, B_N = 1;
   static constexpr bool A_KC = true, B_KC = false;
-  static constexpr int BM = 256, BN = 256;
+  static constexpr int BM = 256, BN = 256, STAGES = 4;
+};
+
+// Two workgroups per CU: a 256 x 128 tile, three stages (72 KiB of LDS each), K steps not a multiple
+// of three (the tail schedule's remainder).
+struct CheckDmaNN2 : CheckDmaNN {
+  static constexpr long K = 2048;
+  static constexpr int BM = 256, BN = 128, STAGES = 3;
 };
 
 struct CheckDmaTN : accy::gemm::Strided<0, 1, 384, 0, 1, 256> {
@@ -54,11 +61,15 @@ struct CheckDmaTN : accy::gemm::Strided<0, 1, 384, 0, 1, 256> {
   static constexpr long M = 384, N = 128, K = 256;
   static constexpr long A_B = 0, A_M = 1, A_K = 384, B_B = 0, B_K = 1, B_N = 256;
   static constexpr bool A_KC = false, B_KC = true;
-  static constexpr int BM = 128, BN = 128;
+  static constexpr int BM = 128, BN = 128, STAGES = 4;
 };
 
 extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_nn(const u16_t* a, const u16_t* b, u16_t* c) {
   accy::gemm::mma16_dma<CheckDmaNN>(a, b, CheckEpi{c, 8192});
+}
+
+extern "C" __global__ void __launch_bounds__(256, 2) accy_check_gemm_dma_nn2(const u16_t* a, const u16_t* b, u16_t* c) {
+  accy::gemm::mma16_dma<CheckDmaNN2>(a, b, CheckEpi{c, 8192});
 }
 
 extern "C" __global__ void __launch_bounds__(256) accy_check_gemm_dma_tn(const u16_t* a, const u16_t* b, u16_t* c) {
@@ -85,7 +96,7 @@ struct CheckDmaMultiAxis {
   static constexpr int DT = 0;
   static constexpr long M = 8192, N = 2048, K = 2048;
   static constexpr bool A_KC = true, B_KC = false;
-  static constexpr int BM = 256, BN = 256;
+  static constexpr int BM = 256, BN = 256, STAGES = 4;
   static __device__ __forceinline__ long a_b(long) { return 0; }
   static __device__ __forceinline__ long a_m(long i) { return (i / 2048) * 4194304L + (i % 2048) * 128L; }
   static __device__ __forceinline__ long a_k(long i) { return (i / 128) * 262144L + (i % 128); }

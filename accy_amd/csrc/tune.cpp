@@ -2,6 +2,8 @@
 // default plan's outputs byte for byte, and timed; the fastest candidate per tunable kernel goes
 // into the tuning table (src/executable/tuning.zig:233-268, recordMeasurements).
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <type_traits>
@@ -82,6 +84,8 @@ size_t tune_program(const Program& program, const void* const* inputs, size_t n_
     for (auto& e : ex) e->invoke_device(inputs, n_inputs, outputs, n_outputs, stream);
   hip_check(hipStreamSynchronize(stream), "hipStreamSynchronize");
 
+  // ACCY_TUNE_REPORT set: every candidate's mean goes to stderr (the artifact keeps the winner only).
+  const bool report = std::getenv("ACCY_TUNE_REPORT") != nullptr;
   size_t recorded = 0;
   for (const Tunable& t : tun) {
     TuningSelection best;
@@ -89,6 +93,9 @@ size_t tune_program(const Program& program, const void* const* inputs, size_t n_
     for (uint32_t c = 0; c < t.count; ++c) {
       const KernelTiming& kt = ex[c]->timings()[t.kernel];
       const uint64_t ns = (uint64_t)((double)kt.mean_ms * 1e6);
+      if (report)
+        std::fprintf(stderr, "tune %s candidate %u of %u: %.1f us over %u calls\n", t.key.c_str(), c, t.count,
+                     kt.mean_ms * 1e3, kt.calls);
       if (!have || ns < best.mean_ns) {
         best = TuningSelection{c, ns, kt.calls};
         have = true;

@@ -12,8 +12,9 @@ import numpy as np
 import pytest
 
 from accy_amd import hip
+from accy_amd import tensor as T
 from accy_amd import workloads as W
-from conftest import assert_normwise, hip_run, oracle_run
+from conftest import assert_normwise, assert_rowwise, hip_run, oracle_run
 
 MAGIC, VERSION = 0x54544341, 1
 
@@ -94,14 +95,14 @@ def test_contraction_follows_the_imported_n_tile():
     src = hip.plan_source(prog)
     (key, cand, count), = tuning_lines(src)
     assert key.startswith("gfx950/gemm/") and (cand, count) == ("0", "2")
-    assert "BN = 256;" in src and "grid 1024 " in src
+    assert "BN = 256, STAGES = 4;" in src and "grid 1024 " in src
     hip.tuning_import(artifact([(key, 2, 1, 10, 3)]))
-    src = hip.plan_source(prog)
-    assert "BN = 128;" in src and "grid 2048 " in src
+    src = hip.plan_source(prog, compile=True)   # the selected candidate builds for gfx950
+    assert "BN = 128, STAGES = 4;" in src and "grid 2048 " in src
     # A record for another key (or candidate count) changes nothing.
     hip.tuning_clear()
     hip.tuning_import(artifact([(key + "x", 2, 1, 10, 3), (key, 3, 1, 10, 3)]))
-    assert "BN = 256;" in hip.plan_source(prog)
+    assert "BN = 256, STAGES = 4;" in hip.plan_source(prog)
 
 
 def test_which_config_kernels_are_tunable():
@@ -133,3 +134,25 @@ def test_tune_on_device_then_compile_takes_the_selection():
     ref = oracle_run(tone, tone_in)[0]
     assert np.all(np.abs(got - ref) <= 1e-5 * np.abs(ref))
     assert_normwise(hip_run(gemm, gemm_in)[0], oracle_run(gemm, gemm_in)[0], 2e-2, "bf16", floor=None)
+
+
+@pytest.mark.gpu
+def test_contraction_candidate_matches_the_default_and_the_oracle():
+    # The 128-column tile against the default 256, with the decoder's GELU epilogue.
+    candidate = 1
+    m, k, n = 512, 2048, 1024
+    prog = T.define("gelu_mm", [T.spec("bf16", m=m, k=k), T.spec("bf16", k=k, n=n)],
+                    lambda b, a: W.gelu(b, a[0].contract(a[1], "k"), "bf16"))
+    rng = np.random.default_rng(21)
+    x = W.to_dtype(rng.standard_normal((m, k)) * 0.5, "bf16")
+    w = W.to_dtype(rng.standard_normal((k, n)) * 0.03, "bf16")
+    default = hip_run(prog, [x, w])[0]
+    (key, cand, count), = tuning_lines(hip.plan_source(prog))
+    assert (cand, count) == ("0", "2")
+    hip.tuning_import(artifact([(key, 2, candidate, 10, 3)]))
+    assert tuning_lines(hip.plan_source(prog)) == [(key, str(candidate), "2")]
+    got = hip_run(prog, [x, w])[0]
+    assert np.array_equal(got, default)       # every output keeps its k order: bit-identical
+    # per row, as for the decoder: GELU's negative tail sits near zero, where one bf16 step of the
+    # pre-activation (a different summation order) is a large relative change of a tiny output
+    assert_rowwise(got, oracle_run(prog, [x, w])[0], 2e-2, "bf16")

@@ -205,8 +205,9 @@ std::string KernelWriter::load_at(int slot, const std::string& base, const std::
   }
 }
 
-std::string KernelWriter::quad_load(int slot, const std::string& var, const std::string& base, DType d) {
+std::string KernelWriter::quad_load(int slot, const std::string& var, const std::string& base, DType d, bool stream) {
   const std::string q = std::string("accy::Quad<") + storage_type(d) + ">";
+  if (stream) return "const " + q + " " + var + " = accy::ld_quad_stream(" + arg(slot, false) + " + " + base + ");";
   return "const " + q + " " + var + " = *(const " + q + "*)(" + arg(slot, false) + " + " + base + ");";
 }
 

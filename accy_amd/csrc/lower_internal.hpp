@@ -65,7 +65,7 @@ class KernelWriter {
   std::string load_at(int slot, const std::string& base, const std::string& idx, DType d);
   // Declaration of an aligned four-element load of slot at element offset base (an accy::Quad), and
   // element idx of such a variable converted to the compute type.
-  std::string quad_load(int slot, const std::string& var, const std::string& base, DType d);
+  std::string quad_load(int slot, const std::string& var, const std::string& base, DType d, bool stream = false);
   static std::string quad_elem(const std::string& var, const std::string& idx, DType d);
   std::string store(int slot, const std::string& off, DType d, const std::string& v);
   std::string tmp();

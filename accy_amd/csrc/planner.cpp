@@ -514,6 +514,36 @@ class Planner {
     std::string hoisted;
     std::map<std::string, std::string> hoisted_var;
     int nquad = 0;
+    // A leaf is streamed (loaded with the non-temporal hint) when this kernel reads each of its
+    // elements exactly once: its buffer holds as many elements as the kernel's rows x row length and
+    // its offset depends on the row (a buffer reached through broadcast_in_dim covers a subset of the
+    // loop's axes, so an equal element count means no axis is broadcast and no element is shared
+    // between rows), and one pass reads it (or the row is cached in registers after the first).
+    auto mentions_row = [](const std::string& off) {
+      for (size_t p = off.find("row"); p != std::string::npos; p = off.find("row", p + 1)) {
+        const bool start = p == 0 || !(isalnum((unsigned char)off[p - 1]) || off[p - 1] == '_');
+        const bool end = p + 3 == off.size() || !(isalnum((unsigned char)off[p + 3]) || off[p + 3] == '_');
+        if (start && end) return true;
+      }
+      return false;
+    };
+    auto streamed = [&](int slot, const std::string& off, DType d, const std::string& key) {
+      if (!commit) return false;
+      const auto use = leaf_use.find(key);
+      const bool once = leaf_array.count(key) > 0 || (use != leaf_use.end() && use->second.size() == 1);
+      const uint64_t elems = plan_.slots[(size_t)slot].bytes / dtype_size(d);
+      return once && elems == kn * tn && mentions_row(off);
+    };
+    // The hoisted vector load of a leaf for this iteration (emitted once per pass), as the lane `u`.
+    auto hoisted_elem = [&](int slot, const std::string& base, DType d, const std::string& key, bool stream) {
+      auto hv = hoisted_var.find(key);
+      if (hv == hoisted_var.end()) {
+        std::string q = "q" + std::to_string(nquad++);
+        hoisted += "      " + w.quad_load(slot, q, base, d, stream) + "\n";
+        hv = hoisted_var.emplace(key, q).first;
+      }
+      return KernelWriter::quad_elem(hv->second, "u", d);
+    };
     w.leaf_hook = [&](int slot, const std::string& off, DType d, Scope& sc, std::string& out) -> bool {
       bool varies = false;
       for (const auto& t : tc)
@@ -525,25 +555,17 @@ class Planner {
       if (it == leaf_array.end()) {
         std::string t = w.tmp();
         std::optional<std::string> base = hoist ? row_rest(off) : std::nullopt;
-        std::string val;
-        if (base) {
-          auto hv = hoisted_var.find(key);
-          if (hv == hoisted_var.end()) {
-            std::string q = "q" + std::to_string(nquad++);
-            hoisted += "      " + w.quad_load(slot, q, *base, d) + "\n";
-            hv = hoisted_var.emplace(key, q).first;
-          }
-          val = KernelWriter::quad_elem(hv->second, "u", d);
-        } else {
-          val = direct_load(slot, off, d);
-        }
+        std::string val = base ? hoisted_elem(slot, *base, d, key, streamed(slot, off, d, key)) : direct_load(slot, off, d);
         sc.out << sc.indent << "const " << compute_type(d) << " " << t << " = " << val << ";\n";
         out = t;
         return true;
       }
       std::string elem = it->second + "[e * " + std::to_string(VEC) + " + u]";
       if (leaf_first[key] == cur_pass) {
-        sc.out << sc.indent << elem << " = " << direct_load(slot, off, d) << ";\n";
+        // The cache is filled by the first pass; a streamed leaf through the hoisted vector load.
+        std::optional<std::string> base = hoist && streamed(slot, off, d, key) ? row_rest(off) : std::nullopt;
+        sc.out << sc.indent << elem << " = " << (base ? hoisted_elem(slot, *base, d, key, true) : direct_load(slot, off, d))
+               << ";\n";
         if (declared.insert(key).second)
           decls += "    " + std::string(compute_type(d)) + " " + it->second + "[" + std::to_string(E * VEC) + "];\n";
       }
@@ -646,6 +668,7 @@ class Planner {
         << w.align_hints() << lds_decl << "  for (I row = blockIdx.x; row < (I)" << kn << "; row += gridDim.x) {\n"
         << decls << body.str() << "  }\n}\n";
     k.source = src.str();
+    k.grid[0] = (uint32_t)std::min<uint64_t>(kn, 1u << 20);
     if (unroll_candidates.size() > 1) {
       k.tuning_key = tuning_key("row", k.source, "rows=" + std::to_string(kn) + ",cols=" + std::to_string(tn));
       k.candidate_count = (uint32_t)unroll_candidates.size();
@@ -655,7 +678,6 @@ class Planner {
         k.source.replace(at, std::strlen(kUnrollMark), pragma);
     }
     k.name = nm;
-    k.grid[0] = (uint32_t)std::min<uint64_t>(kn, 1u << 20);
     k.block[0] = B;
     k.klass = "row";
     k.label = "row:%" + std::to_string(rk.reduces[0]);

@@ -112,6 +112,18 @@ def test_indexing_and_integer_programs_compile():
     assert "__global__" in hip.plan_source(p, compile=True)
 
 
+def test_row_leaves_read_once_are_streamed():
+    # C2 reads each element once (the row is cached in registers): non-temporal vector loads.
+    assert hip.plan_source(W.logsumexp_program(32768, 8192)).count("accy::ld_quad_stream(") == 1
+    # C1's time and sample are broadcast along the rows: every workgroup rereads them, plain loads.
+    assert "ld_quad_stream" not in hip.plan_source(W.tone_program(8192, 16384))
+    # A row too long for the register cache is read by two passes: plain loads.
+    assert "ld_quad_stream" not in hip.plan_source(W.logsumexp_program(64, 102400))
+    # One pass over a row that is not cached (a plain sum): streamed, and it builds for gfx950.
+    p = T.define("rowsum", [T.spec("bf16", r=64, c=65536)], lambda b, a: a[0].sum("c"))
+    assert "accy::ld_quad_stream(" in hip.plan_source(p, compile=True)
+
+
 def test_row_fusion_gives_one_kernel_for_logsumexp():
     src = hip.plan_source(W.logsumexp_program(32, 8192))
     assert src.count("__global__") == 1

@@ -1,0 +1,64 @@
+"""Elementwise (map) kernels: four consecutive elements per thread when the innermost extent is a
+multiple of 4, with operands read at `rest + c` loaded as one vector (non-temporal when read once);
+otherwise one element per thread. Elementwise arithmetic without transcendentals is bit-exact with
+the oracle (runCpu's per-operation arithmetic; src/preparation/kernelization/lowering/elementwise.zig);
+the device's transcendentals are checked against float64 elsewhere."""
+import numpy as np
+import pytest
+
+from accy_amd import hip
+from accy_amd import tensor as T
+from accy_amd import workloads as W
+from conftest import hip_run, oracle_run
+
+F32 = T.Type("f32", ())
+
+
+def mixed(rows, cols):
+    """Each element size (i1 / u8 storage 1 B, bf16 2 B, f32 and i32 4 B, f64 8 B), a row operand
+    broadcast over the rows, and a transposed operand (innermost stride not 1: element loads)."""
+    def body(b, a):
+        x, y, row, h, d, k, xt = a
+        s = x.mul(y).add(row).mul(x)
+        m = x.compare("gt", y)
+        return [s, m, m.select(x, y), h.add(h).mul(h), d.mul(d).add(d), k.add(k),
+                x.add(xt)]
+    specs = [T.spec("f32", r=rows, c=cols), T.spec("f32", r=rows, c=cols), T.spec("f32", c=cols),
+             T.spec("bf16", r=rows, c=cols), T.spec("f64", r=rows, c=cols), T.spec("i32", r=rows, c=cols),
+             T.spec("f32", c=cols, r=rows)]
+    return T.define("mixed", specs, body)
+
+
+def mixed_inputs(rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    return [f(rows, cols), f(rows, cols), f(cols), W.to_dtype(rng.standard_normal((rows, cols)), "bf16"),
+            rng.standard_normal((rows, cols)), rng.integers(-2 ** 30, 2 ** 30, (rows, cols)).astype(np.int32),
+            f(cols, rows)]
+
+
+def test_map_kernels_take_four_elements_per_thread():
+    src = hip.plan_source(mixed(64, 1024), compile=True)
+    assert "for (I i0 = " in src and "accy::ld_quad_stream(" in src
+    # the row operand is shared by all rows: a plain vector load
+    assert "*(const accy::Quad<float>*)(" in src
+    # an innermost extent that is not a multiple of 4: one element per thread
+    src = hip.plan_source(mixed(8, 30), compile=True)
+    assert "for (I i0 = " not in src and "for (I i = " in src
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (3, 8), (8, 30), (1, 4), (257, 132)])
+def test_map_kernels_bit_exact(rows, cols):
+    prog, ins = mixed(rows, cols), mixed_inputs(rows, cols, seed=rows * 1000 + cols)
+    got, ref = hip_run(prog, ins), oracle_run(prog, ins)
+    for i, (g, r) in enumerate(zip(got, ref)):
+        assert np.array_equal(g, r, equal_nan=True), f"output {i}"
+
+
+@pytest.mark.gpu
+def test_large_copy_through_the_vector_map():
+    n = 1 << 26
+    prog = T.define("copy", [T.spec("f32", n=n)], lambda b, a: a[0].mul(b.full_float(F32, 1.0)))
+    x = np.random.default_rng(3).standard_normal(n).astype(np.float32)
+    assert np.array_equal(hip_run(prog, [x])[0], x)

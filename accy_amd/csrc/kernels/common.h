@@ -171,6 +171,12 @@ template <typename T, typename U> __device__ __forceinline__ T wmul(T a, T b) { 
 template <typename T> __device__ __forceinline__ T idiv(T a, T b) { return b == 0 ? (T)0 : ((b == (T)-1) ? (T)(0 - a) : (T)(a / b)); }
 template <typename T> __device__ __forceinline__ T imax(T a, T b) { return a > b ? a : b; }
 template <typename T> __device__ __forceinline__ T imin(T a, T b) { return a < b ? a : b; }
+// A serial fold's float max / min step, as runCpu's x86 code computes it (maxss / minss, then a NaN
+// result replaced by the first operand): the first operand when it is strictly greater (smaller) or
+// the second is NaN, otherwise the second, so a tie (+0 / -0 included) keeps the later element and
+// NaN elements are skipped. (v_max_f32 orders -0 below +0 and would keep +0 on such a tie.)
+template <typename T> __device__ __forceinline__ T fold_max(T a, T b) { return (a > b || b != b) ? a : b; }
+template <typename T> __device__ __forceinline__ T fold_min(T a, T b) { return (a < b || b != b) ? a : b; }
 
 // ---- reduction operators ----
 struct SumOp {

@@ -88,6 +88,10 @@ std::string acc_type(DType d, Reducer r) {
   return compute_type(d);
 }
 
+// The step of a serial fold (fold and chunked fold kernels): as fold_step, with float max / min that
+// keep the later element on ties, as runCpu's fold does (accy::fold_max / fold_min).
+std::string serial_fold_step(DType d, Reducer r, const std::string& acc, const std::string& x);
+
 std::string fold_step(DType d, Reducer r, const std::string& acc, const std::string& x) {
   if (is_float_domain(d)) {
     if (r == Reducer::sum) return acc + " + " + x;
@@ -99,6 +103,12 @@ std::string fold_step(DType d, Reducer r, const std::string& acc, const std::str
   }
   if (r == Reducer::sum) return acc + " + (" + acc_type(d, r) + ")" + x;
   return std::string(r == Reducer::max ? "accy::imax(" : "accy::imin(") + acc + ", " + x + ")";
+}
+
+std::string serial_fold_step(DType d, Reducer r, const std::string& acc, const std::string& x) {
+  if ((is_float_domain(d) || d == DType::f64) && r != Reducer::sum)
+    return std::string(r == Reducer::max ? "accy::fold_max(" : "accy::fold_min(") + acc + ", " + x + ")";
+  return fold_step(d, r, acc, x);
 }
 
 class Planner {
@@ -391,6 +401,14 @@ class Planner {
     uint64_t nred = prod(rdims, 0, rdims.size());
     Reducer r = (Reducer)op.code;
     DType d = rt.dtype;
+    // Few outputs over a long reduced range: one serial fold per output cannot fill the GPU (and keeps
+    // too few loads in flight), so the range is folded in chunks and the chunks' partials folded in
+    // order (fold_chunked).
+    if (nred >= 1024 && nout * nred >= (1ull << 22) && nout < (1ull << 18) && chunk_identity(d, r)) {
+      fold_chunked(v, out, in, red, keep, rdims, kdims, nout, nred, r, d);
+      finish(v);
+      return;
+    }
     KernelWriter w(g_, slots_, itype());
     std::ostringstream body;
     Scope outer(body, "    ");
@@ -405,7 +423,7 @@ class Planner {
     for (size_t i = 0; i < red.size(); ++i) full[red[i]] = rc[i];
     for (size_t i = 0; i < keep.size(); ++i) full[keep[i]] = kc[i];
     std::string x = w.value(op.args[0], full, inner);
-    body << "      acc = " << fold_step(d, r, "acc", x) << ";\n    }\n";
+    body << "      acc = " << serial_fold_step(d, r, "acc", x) << ";\n    }\n";
     std::string res = is_int(d) ? "(" + std::string(compute_type(d)) + ")acc" : round_to(d, "acc");
     body << "    " << w.store(out, "o", d, res) << "\n";
     const uint32_t B = 256;
@@ -425,6 +443,111 @@ class Planner {
     k.label = "fold:%" + std::to_string(v);
     push(std::move(k), w);
     finish(v);
+  }
+
+  // The value a chunk's fold starts from, so that folding the chunks' partials in order from the
+  // program's init gives the serial fold's result: -0 for a float sum (x + -0 = x for every x,
+  // including -0), NaN for a float max / min (fold_max / fold_min skip a NaN second operand and return
+  // the second operand when the first is NaN, so NaN is the absent element; ties keep the later
+  // element, which the in-order combination of the chunks preserves), 0 for a
+  // wrapping integer sum, the type's extreme for an integer max / min. Integer folds and float max /
+  // min are then bit-identical to the serial fold; a float sum is associated differently (within the
+  // reductions' 1e-5 relative bound). Empty for other dtypes.
+  static std::optional<std::string> chunk_identity(DType d, Reducer r) {
+    if (is_float_domain(d)) return std::string(r == Reducer::sum ? "-0.0f" : "__builtin_nanf(\"\")");
+    if (d == DType::f64) return std::string(r == Reducer::sum ? "-0.0" : "__builtin_nan(\"\")");
+    if (r == Reducer::sum && (d == DType::i32 || d == DType::u32 || d == DType::i64 || d == DType::u64))
+      return "(" + acc_type(d, r) + ")0";
+    const bool mx = r == Reducer::max;
+    switch (d) {
+      case DType::i32: return std::string(mx ? "(-2147483647 - 1)" : "2147483647");
+      case DType::u32: return std::string(mx ? "0u" : "4294967295u");
+      case DType::i64: return std::string(mx ? "(-9223372036854775807LL - 1)" : "9223372036854775807LL");
+      case DType::u64: return std::string(mx ? "0ull" : "18446744073709551615ull");
+      default: return std::nullopt;
+    }
+  }
+
+  // Partial dtype of a chunked fold: f32 for the 16-bit floats and f32, f64, the unsigned type for a
+  // wrapping integer sum, the dtype itself for an integer max / min.
+  static DType partial_dtype(DType d, Reducer r) {
+    if (is_float_domain(d)) return DType::f32;
+    if (r == Reducer::sum && d == DType::i32) return DType::u32;
+    if (r == Reducer::sum && d == DType::i64) return DType::u64;
+    return d;
+  }
+
+  // Kernel 1: output o, chunk s (blockIdx.y) folds reduced indices [s * chunk, (s + 1) * chunk) in
+  // order from the chunk identity into part[s * nout + o]. Kernel 2: each output folds its S partials
+  // in chunk order from the program's init, then rounds once (16-bit dtypes) and stores.
+  void fold_chunked(uint32_t v, int out, const Type& in, const std::vector<size_t>& red, const std::vector<size_t>& keep,
+                    const std::vector<Dim>& rdims, const std::vector<Dim>& kdims, uint64_t nout, uint64_t nred, Reducer r,
+                    DType d) {
+    const Op& op = g_.ops[v];
+    const uint32_t B = 256;
+    uint64_t S = std::max<uint64_t>(2, ((1ull << 20) + nout - 1) / nout);
+    S = std::min<uint64_t>(S, std::min<uint64_t>(nred / 256, 65535));
+    const uint64_t chunk = (nred + S - 1) / S;
+    S = (nred + chunk - 1) / chunk;
+    const DType pd = partial_dtype(d, r);
+    const std::string at = acc_type(d, r);
+    const int part = slots_.add(SlotInfo::Temp, -1, pd, S * nout * dtype_size(pd));
+    {
+      KernelWriter w(g_, slots_, itype());
+      std::ostringstream body;
+      std::vector<std::string> kc = delinearize("o", kdims), rc = delinearize("r", rdims);
+      std::vector<std::string> full(in.rank());
+      for (size_t i = 0; i < red.size(); ++i) full[red[i]] = rc[i];
+      for (size_t i = 0; i < keep.size(); ++i) full[keep[i]] = kc[i];
+      body << "    " << at << " acc = " << *chunk_identity(d, r) << ";\n"
+           << "    const I r0 = s * (I)" << chunk << ";\n"
+           << "    const I r1 = r0 + (I)" << chunk << " < (I)" << nred << " ? r0 + (I)" << chunk << " : (I)" << nred << ";\n"
+           << "#pragma unroll 8\n    for (I r = r0; r < r1; ++r) {\n";
+      Scope inner(body, "      ");
+      std::string x = w.value(op.args[0], full, inner);
+      body << "      acc = " << serial_fold_step(d, r, "acc", x) << ";\n    }\n"
+           << "    " << w.store(part, "s * (I)" + std::to_string(nout) + " + o", pd, "acc") << "\n";
+      std::string nm = name("fold_chunks", v);
+      std::ostringstream src;
+      src << "extern \"C\" __global__ void __launch_bounds__(" << B << ") " << nm << "(" << w.params() << ") {\n"
+          << "  typedef " << w.itype << " I;\n  const I s = (I)blockIdx.y;\n"
+          << "  for (I o = (I)blockIdx.x * " << B << " + threadIdx.x; o < (I)" << nout << "; o += (I)gridDim.x * " << B
+          << ") {\n" << body.str() << "  }\n}\n";
+      KernelStep k;
+      k.source = src.str();
+      k.name = nm;
+      k.grid[0] = grid_for(nout, B, 65536);
+      k.grid[1] = (uint32_t)S;
+      k.block[0] = B;
+      k.klass = "fold";
+      k.label = "fold:%" + std::to_string(v) + " chunks";
+      push(std::move(k), w);
+    }
+    {
+      KernelWriter w(g_, slots_, itype());
+      std::ostringstream body;
+      Scope outer(body, "    ");
+      std::string init = w.value(op.args[1], {}, outer);
+      body << "    " << at << " acc = (" << at << ")" << init << ";\n"
+           << "    for (I s = 0; s < (I)" << S << "; ++s) acc = "
+           << serial_fold_step(d, r, "acc", w.load(part, "s * (I)" + std::to_string(nout) + " + o", pd)) << ";\n";
+      std::string res = is_int(d) ? "(" + std::string(compute_type(d)) + ")acc" : round_to(d, "acc");
+      body << "    " << w.store(out, "o", d, res) << "\n";
+      std::string nm = name("fold", v);
+      std::ostringstream src;
+      src << "extern \"C\" __global__ void __launch_bounds__(" << B << ") " << nm << "(" << w.params() << ") {\n"
+          << "  typedef " << w.itype << " I;\n"
+          << "  for (I o = (I)blockIdx.x * " << B << " + threadIdx.x; o < (I)" << nout << "; o += (I)gridDim.x * " << B
+          << ") {\n" << body.str() << "  }\n}\n";
+      KernelStep k;
+      k.source = src.str();
+      k.name = nm;
+      k.grid[0] = grid_for(nout, B, 65536);
+      k.block[0] = B;
+      k.klass = "fold";
+      k.label = "fold:%" + std::to_string(v);
+      push(std::move(k), w);
+    }
   }
 
   // ---- row group: fused reductions over trailing axes of one row space, one workgroup per row ----

@@ -646,6 +646,19 @@ class Planner {
     uint32_t B = lanes >= 256 ? 256 : (uint32_t)std::max<uint64_t>(64, (lanes + 63) / 64 * 64);
     uint64_t E = (tn + (uint64_t)B * VEC - 1) / ((uint64_t)B * VEC);
     size_t passes = rk.reduces.size() + (rk.full_vals.empty() ? 0 : 1);
+    // A row read by several passes is kept in registers when each thread holds at most 64 of its
+    // elements; a row too long for that with 256 threads takes 512 or 1024 threads if that makes it
+    // fit (read once instead of once per pass; four waves per SIMD still have 128 registers each).
+    if (passes >= 2 && E * VEC > 64) {
+      for (uint32_t wide : {512u, 1024u}) {
+        const uint64_t e = (tn + (uint64_t)wide * VEC - 1) / ((uint64_t)wide * VEC);
+        if (e * VEC <= 64) {
+          B = wide;
+          E = e;
+          break;
+        }
+      }
+    }
     bool unrolled = E * VEC <= 64;
     bool cache = unrolled && passes >= 2;
     bool guard = tn % ((uint64_t)B * VEC) != 0;

@@ -10,9 +10,8 @@ import pytest
 
 from accy_amd import hip
 from accy_amd import tensor as T
-from conftest import hip_run, oracle_run
-
-AXES = {"a": None, "b": None, "c": None}
+from accy_amd import workloads as W
+from conftest import assert_normwise, hip_run, oracle_run
 
 
 def _program(seed, dtype):
@@ -87,3 +86,57 @@ def test_random_programs_match_the_oracle(seed, dtype):
         else:
             scale = float(np.abs(r).max()) if r.size else 0.0
             assert np.all(np.abs(g.astype(np.float64) - r) <= 1e-5 * max(scale, 1e-30)), f"output {i}"
+
+
+def _contraction_program(seed, dtype):
+    """A[m, k] . B[k, n] on whichever contraction path the extents select (direct-to-LDS MFMA,
+    register-staged MFMA with edge guards, or the serial-k dot), followed by random elementwise work
+    (some of it fused into the contraction's epilogue), a transposed operand and a reduction."""
+    rng = np.random.default_rng(1000 + seed)
+    m, k, n = (int(rng.choice([16, 48, 128, 160, 256, 512])) for _ in range(3))
+    specs = [T.spec(dtype, m=m, k=k), T.spec(dtype, k=k, n=n), T.spec(dtype, n=n, m=m)]
+    scalar = T.Type(dtype, ())
+
+    def body(b, a):
+        x, w, c = a
+        d = x.contract(w, "k")
+        for _ in range(int(rng.integers(0, 4))):
+            op = str(rng.choice(["add_c", "mul_half", "max0", "tanh", "sub_c"]))
+            if op == "add_c":
+                d = d.add(c)                      # c is [n, m]: a transposed operand
+            elif op == "sub_c":
+                d = d.sub(c)
+            elif op == "mul_half":
+                d = d.mul(b.full_float(scalar, 0.5))
+            elif op == "max0":
+                d = d.max(b.full_float(scalar, 0.0))
+            else:
+                d = d.tanh()
+        outs = [d]
+        if rng.random() < 0.5:
+            outs.append(d.sum(str(rng.choice(["m", "n"]))))
+        return outs
+
+    prog = T.define(f"mm{seed}", specs, body)
+    inputs = [W.to_dtype(rng.standard_normal(t.shape) * sc, dtype)
+              for t, sc in zip(prog.input_types(), (1.0, 1.0 / np.sqrt(k), 1.0))]
+    return prog, inputs
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_contraction_programs_plan_and_compile(seed):
+    for dtype in ("f32", "bf16"):
+        prog, _ = _contraction_program(seed, dtype)
+        assert isinstance(hip.plan_source(prog, compile=True), str)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(24))
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_random_contraction_programs_match_the_oracle(seed, dtype):
+    prog, inputs = _contraction_program(seed, dtype)
+    print(f"seed {seed} {dtype}: inputs {[t.shape for t in prog.input_types()]}", flush=True)
+    got, ref = hip_run(prog, inputs), oracle_run(prog, inputs)
+    tol = 1e-3 if dtype == "f32" else 2e-2
+    for g, r in zip(got, ref):
+        assert_normwise(g, r, tol, dtype, floor=None)

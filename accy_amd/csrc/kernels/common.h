@@ -28,7 +28,13 @@ __device__ __forceinline__ u16_t f32_to_f16(float x) { return __builtin_bit_cast
 __device__ __forceinline__ float bf16_to_f32(u16_t h) { return __builtin_bit_cast(float, ((u32_t)h) << 16); }
 __device__ __forceinline__ u16_t f32_to_bf16(float x) { return __builtin_bit_cast(u16_t, (__bf16)x); }
 __device__ __forceinline__ float round_f16(float x) { return (float)(_Float16)x; }
-__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
+// One v_cvt_pk_bf16_f32 of the pair {0, x}: bf16(x) (nearest even) lands in the high half over a
+// zero low half, which is the f32 value of the rounded x, with no shift back.
+typedef float f32x2_rt __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_rt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float round_bf16(float x) {
+  return __builtin_bit_cast(float, __builtin_convertvector((f32x2_rt){0.0f, x}, bf16x2_rt));
+}
 
 // ---- loads and stores in the compute domain (f32 for 16-bit floats) ----
 template <typename I> __device__ __forceinline__ float ld_f16(const u16_t* __restrict__ p, I i) { return f16_to_f32(p[i]); }

@@ -1531,8 +1531,10 @@ class Planner {
       }
     }
     if (targets.size() != 1) return false;
-    target = *targets.begin();
-    return !done_[target];
+    const uint32_t u = *targets.begin();
+    if (done_[u]) return false;
+    target = u;
+    return true;
   }
 
   // Writes the contraction described by gs into the slot of value v (laid out per os), or, with a

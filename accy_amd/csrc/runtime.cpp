@@ -74,8 +74,12 @@ std::vector<char> compile_kernel_source(const std::string& source, const std::st
   // Packed-f32 instructions stay disabled for every kernel this target builds. A source that
   // contains the line kMfmaVgprForm asks for MFMA results in VGPRs (the fused attention kernel,
   // whose VALU softmax reads every score: with accumulators in AGPRs each read is an extra copy).
+  // The unroll threshold: loops marked `#pragma unroll` unroll whatever their size (a register-held
+  // array indexed by the loop counter, such as a contraction's accumulator tile or a row cache, stays
+  // in registers only when its loop unrolls fully; past LLVM's default size limit the loop stays and
+  // the array moves to scratch memory).
   std::vector<const char*> opts = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
-                                   "-Xclang", "-packed-fp32-ops"};
+                                   "-Xclang", "-packed-fp32-ops", "-mllvm", "-pragma-unroll-threshold=65536"};
   if (source.find(kMfmaVgprForm) != std::string::npos) {
     opts.push_back("-mllvm");
     opts.push_back("-amdgpu-mfma-vgpr-form");

@@ -292,33 +292,48 @@ struct Strided {
 
 // Issues load instruction i of this wave's share of one operand tile (ROWS * 64 bytes, 1 KiB per
 // wave instruction, INSTRS / 4 instructions per wave). KC: rows of 32 k (64 bytes); else rows of k.
-template <int ROWS, bool KC, class O>
+// RMAX is the operand's row extent (M or N). When it is not a multiple of the tile the last tile
+// reaches past it: a row past the end reads the last row (KC), a 16-byte chunk past the end of a k
+// row reads the last chunk (RMAX a multiple of 8), so every load stays inside the operand; those
+// rows and columns only feed outputs that the epilogue does not store.
+template <int ROWS, bool KC, class O, long RMAX>
 __device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave,
                                          int lane, int i) {
   constexpr int INSTRS = ROWS * 64 / 1024;
   static_assert(INSTRS % 4 == 0, "four waves share the tile");
+  constexpr bool RAGGED = RMAX % ROWS != 0;
   const int gi = wave * (INSTRS / 4) + i;
   const u16_t* src;
   if constexpr (KC) {
     const int q = (lane & 7) ^ (lane >> 3);  // logical slot of this lane's physical chunk
     const int row = 16 * gi + 2 * (lane >> 3) + (q >> 2);
-    src = base + O::row(r0 + row) + O::k(k0) + 8 * (q & 3);
+    long r = r0 + row;
+    if constexpr (RAGGED) r = r < RMAX ? r : RMAX - 1;
+    src = base + O::row(r) + O::k(k0) + 8 * (q & 3);
   } else {
+    static_assert(!RAGGED || RMAX % 8 == 0, "whole 16-byte chunks");
     constexpr int ROWB = ROWS * 2;    // bytes per k row
     constexpr int LPR = ROWB / 16;    // lanes per k row
     constexpr int RPI = 1024 / ROWB;  // k rows per instruction
     const int row = RPI * gi + lane / LPR;
     const int p = lane % LPR;
     const int u = (p >> 1) ^ (row & 7);
-    src = base + O::k(k0 + row) + O::row(r0) + 16 * u + 8 * (p & 1);
+    if constexpr (RAGGED) {
+      long col = r0 + 16 * u + 8 * (p & 1);
+      col = col <= RMAX - 8 ? col : RMAX - 8;
+      src = base + O::k(k0 + row) + O::row(col);
+    } else {
+      // whole tiles lie inside one contiguous run of the row group: affine there
+      src = base + O::k(k0 + row) + O::row(r0) + 16 * u + 8 * (p & 1);
+    }
   }
   dma16(src, (ACCY_LDS void*)(lds + gi * 512));
 }
 
-template <int ROWS, bool KC, class O>
+template <int ROWS, bool KC, class O, long RMAX>
 __device__ __forceinline__ void dma_tile(const u16_t* __restrict__ base, long r0, long k0, u16_t* lds, int wave, int lane) {
 #pragma unroll
-  for (int i = 0; i < ROWS * 64 / 1024 / 4; ++i) dma_part<ROWS, KC, O>(base, r0, k0, lds, wave, lane, i);
+  for (int i = 0; i < ROWS * 64 / 1024 / 4; ++i) dma_part<ROWS, KC, O, RMAX>(base, r0, k0, lds, wave, lane, i);
 }
 
 // Fragment of 32 rows (M or N) x 16 k for one MFMA, read from a stage.
@@ -397,9 +412,9 @@ struct DmaStep {
         if (k < NF) {
           f1.load_one(k, as[STAGE], bs[STAGE], 1, lane, wm, wn);
         } else if (k - NF < DA) {
-          dma_part<C::BM, C::A_KC, AOff<C>>(Ab, m0, (kt + S - 1) * 32, as[NEXT], wave, lane, k - NF);
+          dma_part<C::BM, C::A_KC, AOff<C>, C::M>(Ab, m0, (kt + S - 1) * 32, as[NEXT], wave, lane, k - NF);
         } else {
-          dma_part<C::BN, C::B_KC, BOff<C>>(Bb, n0, (kt + S - 1) * 32, bs[NEXT], wave, lane, k - NF - DA);
+          dma_part<C::BN, C::B_KC, BOff<C>, C::N>(Bb, n0, (kt + S - 1) * 32, bs[NEXT], wave, lane, k - NF - DA);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -456,7 +471,8 @@ struct DmaGroup {
   }
 };
 
-// Requires M % BM == 0, N % BN == 0, K % 32 == 0 with at least STAGES K steps, 16-byte aligned rows;
+// Requires K % 32 == 0 with at least STAGES K steps and 16-byte aligned rows (M or N not a multiple
+// of the tile: see dma_part);
 // 256 threads (2 x 2 waves). LDS: STAGES x (BM + BN) x 64 bytes (STAGES = 4 with a 256 x 256 tile:
 // 128 KiB, one workgroup per CU; 3 with 256 x 128: 72 KiB, two per CU when the kernel is compiled for
 // two waves per SIMD, so that one workgroup's epilogue runs beside the other's matrix work).
@@ -464,8 +480,8 @@ template <class C, class Epi>
 __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi) {
   constexpr int BM = C::BM, BN = C::BN, S = C::STAGES;
   constexpr int TM = BM / 64, TN = BN / 64;
-  constexpr long TILES_M = C::M / BM, TILES_N = C::N / BN, KT = C::K / 32;
-  static_assert(C::M % BM == 0 && C::N % BN == 0 && C::K % 32 == 0, "exact tiles only");
+  constexpr long TILES_M = (C::M + BM - 1) / BM, TILES_N = (C::N + BN - 1) / BN, KT = C::K / 32;
+  static_assert(C::K % 32 == 0, "whole K steps");
   static_assert(S >= 2 && S <= 4 && KT >= S, "two to four stages, at least one K step per stage");
   constexpr int PER = (BM * 64 / 1024) / 4 + (BN * 64 / 1024) / 4;  // DMA instructions per wave per step
   static_assert((S - 2) * PER < 64, "vmcnt range");
@@ -499,8 +515,8 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
 
 #pragma unroll
   for (int s = 0; s < S - 1; ++s) {
-    dma_tile<BM, C::A_KC, AOff<C>>(Ab, m0, s * 32, as[s], wave, lane);
-    dma_tile<BN, C::B_KC, BOff<C>>(Bb, n0, s * 32, bs[s], wave, lane);
+    dma_tile<BM, C::A_KC, AOff<C>, C::M>(Ab, m0, s * 32, as[s], wave, lane);
+    dma_tile<BN, C::B_KC, BOff<C>, C::N>(Bb, n0, s * 32, bs[s], wave, lane);
   }
   // Tile 0 complete everywhere (tiles 1 .. S - 2 may still be in flight), then its first sub-step.
   Frags<C> f0;
@@ -525,7 +541,10 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) epi(batch, row_base + i * 32 + g * 8 + r, col_base + j * 32, acc[i][j][g * 4 + r]);
+        for (int r = 0; r < 4; ++r) {
+          const long m = row_base + i * 32 + g * 8 + r, n = col_base + j * 32;
+          if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) epi(batch, m, n, acc[i][j][g * 4 + r]);
+        }
 }
 
 

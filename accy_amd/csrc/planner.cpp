@@ -1097,11 +1097,20 @@ class Planner {
   }
 
   bool dma_eligible(const GemmShape& gs, int& dm, int& dn, bool& a_kc, bool& b_kc) const {
+    // whole K steps of 32, at least as many as pipeline stages
+    if (gs.k % 32 != 0 || gs.k < 128 || std::getenv("ACCY_GEMM_NO_DMA")) return false;
     dm = dma_rows(gs.m);
     dn = dma_rows(gs.n);
-    if (!dm || !dn || gs.k % 128 != 0 || std::getenv("ACCY_GEMM_NO_DMA")) return false;
-    return dma_operand(gs.ga_m, gs.ga_k, gs.ga_b, gs.a.offset, dm, a_kc) &&
-           dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, dn, b_kc);
+    if (dm && dn)
+      return dma_operand(gs.ga_m, gs.ga_k, gs.ga_b, gs.a.offset, dm, a_kc) &&
+             dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, dn, b_kc);
+    // M or N not a multiple of 128: single-axis groups with extents a multiple of 8, tiles that reach
+    // past the end (the kernel clamps those loads to the last row / chunk and stores only in range).
+    if (gs.multi || gs.m % 8 != 0 || gs.n % 8 != 0) return false;
+    dm = dm ? dm : (gs.m > 128 ? 256 : 128);
+    dn = dn ? dn : (gs.n > 128 ? 256 : 128);
+    return dma_operand(gs.ga_m, gs.ga_k, gs.ga_b, gs.a.offset, 8, a_kc) &&
+           dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, 8, b_kc);
   }
 
   // The MFMA templates take 16-bit operands whose K or M/N stride is 1, with 8-element aligned rows
@@ -1691,7 +1700,7 @@ class Planner {
         put("ACCY_LAUNCH_BOUNDS", "__launch_bounds__(" + std::to_string(threads) +
                                       (c.occupancy > 1 ? ", " + std::to_string(c.occupancy) : "") + ")");
       }
-      int64_t tiles = dma ? (gs.m / dm) * (gs.n / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
+      int64_t tiles = dma ? ((gs.m + dm - 1) / dm) * ((gs.n + dn - 1) / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
       k.grid[0] = (uint32_t)tiles;
       k.block[0] = threads;
       k.shared_bytes = dma ? 0u : 2u * (BM + BN) * (BK + 8) * 2u;

@@ -279,9 +279,13 @@ def test_gemm_mfma_transposed_lhs():
 
 
 @pytest.mark.parametrize("case", ["nn-256x512x384-bf16", "nn-128x256x128-f16", "tn-384x256x128-bf16",
-                                  "nt-batched-256x128x384-f16"])
+                                  "nt-batched-256x128x384-f16",
+                                  # M / N not multiples of the tile (last tiles clamp their loads and
+                                  # store only in range), K a multiple of 32 only
+                                  "nn-1000x1056x1000-bf16", "nn-264x160x136-f16", "tn-200x288x392-bf16",
+                                  "nt-batched-136x160x264-f16", "nn-8x128x8-bf16"])
 def test_gemm_direct_to_lds_layouts(case):
-    """Shapes the direct-to-LDS pipeline takes (exact tiles), in each operand layout."""
+    """Shapes the direct-to-LDS pipeline takes, in each operand layout."""
     say(f"gemm dma {case}")
     kind, shape, dtype = case.split("-")[0], case.split("-")[-2], case.split("-")[-1]
     m, k, n = map(int, shape.split("x"))

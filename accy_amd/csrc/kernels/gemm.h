@@ -584,16 +584,21 @@ __device__ __forceinline__ void f32_issue(const float* __restrict__ Ab, const fl
     const int gi = wave * 8 + i;  // 1 KiB per instruction: 8 A rows, or 1 B row
     const int row = 8 * gi + (lane >> 3);
     const int c = (lane & 7) ^ ((row >> 1) & 7);
-    dma16(Ab + C::a_m(m0 + row) + C::a_k(k0) + 4 * c, (ACCY_LDS void*)(as + gi * 256));
-    dma16(Bb + C::b_k(k0 + gi) + C::b_n(n0) + 4 * lane, (ACCY_LDS void*)(bs + gi * 256));
+    // Past the end of M (N) the last tile reads the last row (last 4-float chunk): every load stays
+    // inside the operand, and those rows and columns only feed outputs that are not stored.
+    long r = m0 + row, col = n0 + 4 * lane;
+    if constexpr (C::M % 256 != 0) r = r < C::M ? r : C::M - 1;
+    if constexpr (C::N % 256 != 0) col = col <= C::N - 4 ? col : C::N - 4;
+    dma16(Ab + C::a_m(r) + C::a_k(k0) + 4 * c, (ACCY_LDS void*)(as + gi * 256));
+    dma16(Bb + C::b_k(k0 + gi) + C::b_n(col), (ACCY_LDS void*)(bs + gi * 256));
   }
 }
 
 template <class C, class Epi>
 __device__ __forceinline__ void mma32f(const float* __restrict__ A, const float* __restrict__ B, const Epi& epi) {
   constexpr int BM = 256, BN = 256, BKF = 32;
-  constexpr long TILES_M = C::M / BM, TILES_N = C::N / BN, KT = C::K / BKF;
-  static_assert(C::M % BM == 0 && C::N % BN == 0 && C::K % BKF == 0, "exact tiles only");
+  constexpr long TILES_M = (C::M + BM - 1) / BM, TILES_N = (C::N + BN - 1) / BN, KT = C::K / BKF;
+  static_assert(C::K % BKF == 0 && C::N % 4 == 0, "whole K steps, 16-byte chunks of B rows");
   __shared__ __attribute__((aligned(1024))) float a0[BM * BKF], a1[BM * BKF];
   __shared__ __attribute__((aligned(1024))) float b0[BKF * BN], b1[BKF * BN];
 
@@ -659,7 +664,10 @@ __device__ __forceinline__ void mma32f(const float* __restrict__ A, const float*
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) epi(batch, row_base + i * 32 + g * 8 + r, col_base + j, acc[i][j][g * 4 + r]);
+        for (int j = 0; j < 4; ++j) {
+          const long m = row_base + i * 32 + g * 8 + r, n = col_base + j;
+          if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) epi(batch, m, n, acc[i][j][g * 4 + r]);
+        }
 }
 
 }  // namespace gemm

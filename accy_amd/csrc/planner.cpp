@@ -1122,10 +1122,13 @@ class Planner {
     if (!gemm_shape(op, gs)) return false;
     if (gs.m * gs.n * gs.k == 0) return false;
     if (d == DType::f32) {
-      // The f32 MFMA kernel: exact 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with
-      // 16-byte aligned rows; other f32 contractions keep runCpu's serial k order.
+      // The f32 MFMA kernel: 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with 16-byte
+      // aligned rows. Exact tiles, or M / N off the tile grid (N a multiple of 4) when the problem is
+      // large (2^27 multiply-adds and more); other f32 contractions keep runCpu's serial k order.
       auto ok4 = [](int64_t x) { return x % 4 == 0; };
-      return !gs.multi && gs.m % 256 == 0 && gs.n % 256 == 0 && gs.k % 32 == 0 && gs.a_k == 1 && gs.b_n == 1 &&
+      const bool exact = gs.m % 256 == 0 && gs.n % 256 == 0;
+      const bool large = (double)gs.m * (double)gs.n * (double)gs.k * (double)gs.batch >= (double)(1ull << 27);
+      return !gs.multi && (exact || (large && gs.n % 4 == 0)) && gs.k % 32 == 0 && gs.a_k == 1 && gs.b_n == 1 &&
              ok4(gs.a_m) && ok4(gs.b_k) && ok4(gs.a_b) && ok4(gs.b_b) && ok4(gs.a.offset) && ok4(gs.b.offset);
     }
     if (gs.multi) {
@@ -1628,7 +1631,7 @@ class Planner {
       src << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << w->params() << ") {\n"
           << "  accy::gemm::mma32f<Cfg_" << nm << ">(" << a << " + " << gs.a.offset << "L, " << b << " + "
           << gs.b.offset << "L, Epi_" << nm << "{" << inits.str() << "});\n}\n";
-      k.grid[0] = (uint32_t)((gs.m / 256) * (gs.n / 256));
+      k.grid[0] = (uint32_t)(((gs.m + 255) / 256) * ((gs.n + 255) / 256));
       k.block[0] = 256;
     } else {
       // 256 x 256 x 64 tiles; the wave grid (4 x 2 waves of 64 x 128, or 2 x 2 waves of 128 x 128)

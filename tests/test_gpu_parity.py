@@ -311,7 +311,10 @@ def _gemm_kernels(prog):
 
 
 @pytest.mark.parametrize("m,k,n,spelling", [(512, 96, 256, "contract"), (256, 64, 512, "mulsum"),
-                                            (768, 32, 256, "mulsum"), (256, 8192, 256, "contract")])
+                                            (768, 32, 256, "mulsum"), (256, 8192, 256, "contract"),
+                                            # large and off the tile grid: clamped loads, guarded stores
+                                            (1000, 1024, 1000, "contract"), (520, 1024, 516, "mulsum"),
+                                            (33, 8192, 1028, "contract")])
 def test_gemm_f32_on_mfma(m, k, n, spelling):
     say(f"gemm f32 {m}x{k}x{n} {spelling}")
     prog = W.gemm_program(m, k, n, "f32", spelling)

@@ -1113,6 +1113,81 @@ class Planner {
            dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, 8, b_kc);
   }
 
+  // The f32 MFMA kernel's operand layouts: A K-contiguous, B N-contiguous, rows 16-byte aligned.
+  static bool f32_layout_ok(const GemmShape& gs) {
+    auto ok4 = [](int64_t x) { return x % 4 == 0; };
+    return gs.a_k == 1 && gs.b_n == 1 && ok4(gs.a_m) && ok4(gs.b_k) && ok4(gs.a_b) && ok4(gs.b_b) &&
+           ok4(gs.a.offset) && ok4(gs.b.offset);
+  }
+
+  // Copies an f32 operand view (batch x R x C with strides sb, sr, sc from offset `off` of `slot`) into
+  // a new contiguous temporary [batch][R][C] and returns its slot. One workgroup per 64 x 64 tile: when
+  // the rows are the contiguous axis (sr == 1, a transpose) the tile goes through LDS, read along r and
+  // written along c, so both sides touch whole lines; otherwise element by element along c.
+  int pack_f32(int slot, int64_t off, int64_t batch, int64_t R, int64_t C, int64_t sb, int64_t sr, int64_t sc) {
+    const int dst = slots_.add(SlotInfo::Temp, -1, DType::f32, (uint64_t)(batch * R * C) * 4);
+    KernelWriter w(g_, slots_, "i64_t");
+    const std::string src = w.arg(slot, false), out = w.arg(dst, true);
+    const std::string nm = name("pack", (uint32_t)dst);
+    std::ostringstream k;
+    const int64_t tr = (R + 63) / 64, tc = (C + 63) / 64;
+    k << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << w.params() << ") {\n"
+      << "  const long b = blockIdx.y, r0 = (long)(blockIdx.x / " << tc << ") * 64, c0 = (long)(blockIdx.x % " << tc << ") * 64;\n"
+      << "  const float* __restrict__ s = " << src << " + " << off << "L + b * " << sb << "L;\n"
+      << "  float* __restrict__ d = " << out << " + b * " << R * C << "L;\n";
+    if (sr == 1) {
+      k << "  __shared__ float tile[64][65];\n"
+        << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
+        << "  for (int c = q; c < 64; c += 4)\n"
+        << "    if (r0 + t < " << R << "L && c0 + c < " << C << "L) tile[c][t] = s[(r0 + t) + (c0 + c) * " << sc << "L];\n"
+        << "  __syncthreads();\n"
+        << "  for (int r = q; r < 64; r += 4)\n"
+        << "    if (r0 + r < " << R << "L && c0 + t < " << C << "L) d[(r0 + r) * " << C << "L + c0 + t] = tile[t][r];\n";
+    } else {
+      k << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
+        << "  for (int r = q; r < 64; r += 4)\n"
+        << "    if (r0 + r < " << R << "L && c0 + t < " << C << "L) d[(r0 + r) * " << C << "L + c0 + t] = s[(r0 + r) * " << sr
+        << "L + (c0 + t) * " << sc << "L];\n";
+    }
+    k << "}\n";
+    KernelStep ks;
+    ks.source = k.str();
+    ks.name = nm;
+    ks.grid[0] = (uint32_t)(tr * tc);
+    ks.grid[1] = (uint32_t)batch;
+    ks.block[0] = 256;
+    ks.klass = "pack";
+    ks.label = "pack:slot" + std::to_string(slot);
+    ks.algorithmic_bytes = 8.0 * (double)(batch * R * C);
+    push(std::move(ks), w);
+    return dst;
+  }
+
+  // Repacks the operands of a large f32 contraction whose layout the MFMA kernel does not take.
+  void pack_f32_operands(GemmShape& gs) {
+    auto ok4 = [](int64_t x) { return x % 4 == 0; };
+    if (!(gs.a_k == 1 && ok4(gs.a_m) && ok4(gs.a_b) && ok4(gs.a.offset))) {
+      const int s = pack_f32(gs.a.slot, gs.a.offset, gs.batch, gs.m, gs.k, gs.a_b, gs.a_m, gs.a_k);
+      gs.a = View{s, 0, {}};
+      gs.a_b = gs.m * gs.k;
+      gs.a_m = gs.k;
+      gs.a_k = 1;
+      gs.ga_b = Group{{gs.batch}, {gs.a_b}};
+      gs.ga_m = Group{{gs.m}, {gs.a_m}};
+      gs.ga_k = Group{{gs.k}, {1}};
+    }
+    if (!(gs.b_n == 1 && ok4(gs.b_k) && ok4(gs.b_b) && ok4(gs.b.offset))) {
+      const int s = pack_f32(gs.b.slot, gs.b.offset, gs.batch, gs.k, gs.n, gs.b_b, gs.b_k, gs.b_n);
+      gs.b = View{s, 0, {}};
+      gs.b_b = gs.k * gs.n;
+      gs.b_k = gs.n;
+      gs.b_n = 1;
+      gs.gb_b = Group{{gs.batch}, {gs.b_b}};
+      gs.gb_k = Group{{gs.k}, {gs.b_k}};
+      gs.gb_n = Group{{gs.n}, {1}};
+    }
+  }
+
   // The MFMA templates take 16-bit operands whose K or M/N stride is 1, with 8-element aligned rows
   // (or, for operands whose groups span several axes, the direct-to-LDS kernel's layouts).
   bool gemm_eligible(const Op& op, GemmShape& gs) const {
@@ -1125,11 +1200,12 @@ class Planner {
       // The f32 MFMA kernel: 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with 16-byte
       // aligned rows. Exact tiles, or M / N off the tile grid (N a multiple of 4) when the problem is
       // large (2^27 multiply-adds and more); other f32 contractions keep runCpu's serial k order.
-      auto ok4 = [](int64_t x) { return x % 4 == 0; };
+      // Large problems with another operand layout (an A stored M-contiguous, a B stored K-contiguous,
+      // rows not 16-byte aligned) copy that operand into a contiguous temporary first (pack_f32).
       const bool exact = gs.m % 256 == 0 && gs.n % 256 == 0;
       const bool large = (double)gs.m * (double)gs.n * (double)gs.k * (double)gs.batch >= (double)(1ull << 27);
-      return !gs.multi && (exact || (large && gs.n % 4 == 0)) && gs.k % 32 == 0 && gs.a_k == 1 && gs.b_n == 1 &&
-             ok4(gs.a_m) && ok4(gs.b_k) && ok4(gs.a_b) && ok4(gs.b_b) && ok4(gs.a.offset) && ok4(gs.b.offset);
+      if (gs.multi || !(exact || (large && gs.n % 4 == 0)) || gs.k % 32 != 0) return false;
+      return f32_layout_ok(gs) || large;
     }
     if (gs.multi) {
       int dm, dn;
@@ -1492,6 +1568,7 @@ class Planner {
     }
     GemmShape gs;
     if (gemm_eligible(op, gs)) {
+      if (op.result.dtype == DType::f32 && !f32_layout_ok(gs)) pack_f32_operands(gs);
       gemm(v, gs);
       return;
     }

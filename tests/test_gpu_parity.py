@@ -323,6 +323,41 @@ def test_gemm_f32_on_mfma(m, k, n, spelling):
     assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-3, "f32")
 
 
+@pytest.mark.parametrize("case", ["nt-1024x256x1024", "tn-520x512x516", "nt-batched-4x1024x64x1024"])
+def test_gemm_f32_other_layouts_repacked_onto_mfma(case):
+    """Large f32 contractions whose operand layout the f32 kernel does not take (A stored [k, m], B
+    stored [n, k]): the operand is copied into a contiguous temporary (a tiled transpose), then the
+    MFMA kernel runs; 1e-3 normwise, as for every f32 contraction on the matrix cores."""
+    say(f"gemm f32 repacked {case}")
+    parts = case.split("-")
+    if parts[0] == "nt" and parts[1] == "batched":
+        h, m, k, n = map(int, parts[2].split("x"))
+        prog = T.define("ntb", [T.spec("f32", h=h, m=m, k=k), T.spec("f32", h=h, n=n, k=k)],
+                        lambda b, a: a[0].contract(a[1], "k"))
+        ins = [W.normal(41, h * m * k).astype(np.float32).reshape(h, m, k),
+               W.normal(42, h * n * k).astype(np.float32).reshape(h, n, k)]
+    else:
+        m, k, n = map(int, parts[1].split("x"))
+        if parts[0] == "nt":
+            specs = [T.spec("f32", m=m, k=k), T.spec("f32", n=n, k=k)]
+            shapes = [(m, k), (n, k)]
+        else:
+            specs = [T.spec("f32", k=k, m=m), T.spec("f32", k=k, n=n)]
+            shapes = [(k, m), (k, n)]
+        prog = T.define(parts[0], specs, lambda b, a: a[0].contract(a[1], "k"))
+        ins = [W.normal(43 + i, int(np.prod(sh))).astype(np.float32).reshape(sh) for i, sh in enumerate(shapes)]
+    src = hip.plan_source(prog)
+    assert "accy::gemm::mma32f<" in src and "// pack:" in src
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-3, "f32")
+
+
+def test_f32_attention_scores_on_the_matrix_cores():
+    prog = W.attention_program(4, 1024, 64, "f32")
+    assert "accy::gemm::mma32f<" in hip.plan_source(prog)
+    ins = W.attention_inputs(4, 1024, 64, "f32", seed=12)
+    assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-3, "f32")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_gemm_mulsum_16bit_on_mfma(dtype):
     say(f"gemm {dtype} 256x256x512 mulsum")

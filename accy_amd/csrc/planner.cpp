@@ -310,6 +310,8 @@ class Planner {
     const Type& t = g_.type(v);
     uint64_t nel = t.elements();
     if (nel == 0) return;
+    View pv;
+    if (resolve_view(v, pv) && permute_copy(v, slot, pv)) return;
     KernelWriter w(g_, slots_, itype());
     std::ostringstream body;
     const uint32_t B = 256;
@@ -943,6 +945,63 @@ class Planner {
       default:
         return false;
     }
+  }
+
+  // A value that is a permutation of a buffer (a transpose view) whose innermost axis is strided in
+  // the source while another axis r is contiguous there: a copy through LDS, one 64 x 64 tile of
+  // (r, innermost) per workgroup, read along r and written along the innermost axis, so both sides
+  // touch whole lines (an element-wise map would read one line per element). The other axes are
+  // enumerated by blockIdx.y. Raw storage is copied, so any dtype.
+  bool permute_copy(uint32_t v, int slot, const View& pv) {
+    const Type& t = g_.type(v);
+    const size_t n = t.rank();
+    if (n < 2) return false;
+    const int64_t sc = pv.strides[n - 1];
+    if (sc == 1 || sc == 0 || t.dims[n - 1].extent < 16) return false;
+    size_t r = n;
+    for (size_t a = 0; a + 1 < n; ++a)
+      if (pv.strides[a] == 1 && t.dims[a].extent > 1) r = a;
+    if (r == n) return false;
+    const std::vector<int64_t> ds = row_major_strides(t.dims);
+    int64_t outer = 1;
+    for (size_t a = 0; a + 1 < n; ++a)
+      if (a != r) outer *= t.dims[a].extent;
+    if (outer > 65535) return false;
+    const int64_t er = t.dims[r].extent, ec = t.dims[n - 1].extent, tc = (ec + 63) / 64;
+    KernelWriter w(g_, slots_, "i64_t");
+    const std::string src = w.arg(pv.slot, false), dst = w.arg(slot, true);
+    const std::string T = storage_type(t.dtype);
+    std::ostringstream k;
+    const std::string nm = name("permute", v);
+    k << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << w.params() << ") {\n"
+      << "  __shared__ " << T << " tile[64][65];\n"
+      << "  long o = blockIdx.y, so = " << pv.offset << "L, dof = 0;\n";
+    for (size_t a = n - 1; a-- > 0;) {
+      if (a == r) continue;
+      k << "  { const long x = o % " << t.dims[a].extent << "L; o /= " << t.dims[a].extent << "L; so += x * "
+        << pv.strides[a] << "L; dof += x * " << ds[a] << "L; }\n";
+    }
+    k << "  const long r0 = (long)(blockIdx.x / " << tc << ") * 64, c0 = (long)(blockIdx.x % " << tc << ") * 64;\n"
+      << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
+      << "  for (int c = q; c < 64; c += 4)\n"
+      << "    if (r0 + t < " << er << "L && c0 + c < " << ec << "L) tile[c][t] = " << src << "[so + r0 + t + (c0 + c) * " << sc
+      << "L];\n"
+      << "  __syncthreads();\n"
+      << "  for (int r = q; r < 64; r += 4)\n"
+      << "    if (r0 + r < " << er << "L && c0 + t < " << ec << "L) " << dst << "[dof + (r0 + r) * " << ds[r]
+      << "L + c0 + t] = tile[t][r];\n"
+      << "}\n";
+    KernelStep ks;
+    ks.source = k.str();
+    ks.name = nm;
+    ks.grid[0] = (uint32_t)(((er + 63) / 64) * tc);
+    ks.grid[1] = (uint32_t)outer;
+    ks.block[0] = 256;
+    ks.klass = "map";
+    ks.label = "permute:%" + std::to_string(v);
+    ks.algorithmic_bytes = 2.0 * (double)t.bytes();
+    push(std::move(ks), w);
+    return true;
   }
 
   // Collapses a group of dims (in the given order) into one extent and stride, if the group is

@@ -62,3 +62,36 @@ def test_large_copy_through_the_vector_map():
     prog = T.define("copy", [T.spec("f32", n=n)], lambda b, a: a[0].mul(b.full_float(F32, 1.0)))
     x = np.random.default_rng(3).standard_normal(n).astype(np.float32)
     assert np.array_equal(hip_run(prog, [x])[0], x)
+
+
+def test_transposes_are_copied_through_lds_tiles():
+    p = T.define("tr", [T.spec("f32", r=256, c=512)], lambda b, a: b.transpose(a[0], [1, 0]))
+    src = hip.plan_source(p, compile=True)
+    assert "// permute:" in src and "tile[64][65]" in src
+    # the innermost axis contiguous in the source already: the vector map
+    p = T.define("same", [T.spec("f32", a=4, b=64, c=128)], lambda b, a: b.transpose(a[0], [1, 0, 2]))
+    assert "// permute:" not in hip.plan_source(p)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,dims,perm", [
+    ("f32", (("r", 1000), ("c", 3000)), (1, 0)),
+    ("bf16", (("a", 4), ("b", 300), ("c", 130)), (2, 0, 1)),
+    ("f64", (("a", 3), ("b", 65), ("c", 70)), (0, 2, 1)),
+    ("i32", (("a", 2), ("b", 3), ("c", 100), ("d", 64)), (3, 1, 0, 2)),
+    ("i1", (("r", 77), ("c", 129)), (1, 0)),
+])
+def test_transposes_bit_exact(dtype, dims, perm):
+    p = T.define("perm", [T.spec(dtype, *dims)], lambda b, a: b.transpose(a[0], list(perm)))
+    rng = np.random.default_rng(len(dims) * 10 + perm[0])
+    shape = tuple(e for _, e in dims)
+    if dtype == "bf16":
+        x = W.to_dtype(rng.standard_normal(shape), "bf16")
+    elif dtype == "i1":
+        x = rng.random(shape) < 0.5
+    elif dtype == "i32":
+        x = rng.integers(-10 ** 9, 10 ** 9, shape).astype(np.int32)
+    else:
+        x = rng.standard_normal(shape).astype(T.NUMPY_DTYPE[dtype])
+    got, ref = hip_run(p, [x])[0], oracle_run(p, [x])[0]
+    assert np.array_equal(got, ref) and np.array_equal(ref, np.transpose(x, perm))

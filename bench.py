@@ -139,8 +139,8 @@ def config_table():
 
 def oracle_time(cfg, budget_s: float = 8.0):
     """Times the CPU oracle on the config's bounded sample, with all host threads (capped at 16) and
-    with one thread (runCpu launches single-threaded); each until `budget_s` is spent (at most 10
-    runs). The oracle's per-output order makes both bit-identical."""
+    with one thread (runCpu launches single-threaded); each until `budget_s` is spent (at most 50
+    runs; about 16 s of CPU work in all). The oracle's per-output order makes both bit-identical."""
     sys.path.insert(0, str(ROOT / "tests"))
     from conftest import oracle_lib, oracle_run
     prog, ins, work = cfg["sample"]()
@@ -157,7 +157,7 @@ def oracle_time(cfg, budget_s: float = 8.0):
             t0 = time.perf_counter()
             oracle_run(prog, ins)
             times.append(time.perf_counter() - t0)
-            if time.perf_counter() - start >= budget_s or len(times) >= 10:
+            if time.perf_counter() - start >= budget_s or len(times) >= 50:
                 break
         return float(np.median(times)), len(times)
 

@@ -1796,48 +1796,37 @@ class Planner {
           << gs.ga_b.fn("a_b") << gs.ga_m.fn("a_m") << gs.ga_k.fn("a_k") << gs.gb_b.fn("b_b") << gs.gb_k.fn("b_k")
           << gs.gb_n.fn("b_n");
       // Launch candidates of the direct-to-LDS kernel (bit-identical results: every output keeps its
-      // k order): 256 x 256 with 4 stages, one workgroup per CU (128 KiB of LDS), then, where B's
-      // layout allows a 128-column tile, 256 x 128 with 4 stages. (256 x 128 with 3 stages and two
-      // workgroups per CU was measured too: its LDS traffic per MFMA is half as large again as the
-      // 256 x 256 tile's, and it ran 20-40 % slower on every benchmark contraction.) The source
-      // carries placeholders until the candidate is chosen.
-      struct DmaCandidate {
-        int bn, stages, occupancy;
-      };
-      std::vector<DmaCandidate> cands{{dn, 4, 1}};
+      // k order): the N tile, 256 (4 stages, one workgroup per CU, 128 KiB of LDS), then 128 where
+      // B's layout allows it. (256 x 128 with 3 stages and two workgroups per CU was measured too:
+      // its LDS traffic per MFMA is half as large again as the 256 x 256 tile's, and it ran 20-40 %
+      // slower on every benchmark contraction.) The source carries a placeholder until the candidate
+      // is chosen.
+      std::vector<int> n_tiles{dn};
       if (dma && dn == 256) {
         bool kc2 = bkc;
-        if (dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, 128, kc2) && kc2 == bkc) cands.push_back({128, 4, 1});
+        if (dma_operand(gs.gb_n, gs.gb_k, gs.gb_b, gs.b.offset, 128, kc2) && kc2 == bkc) n_tiles.push_back(128);
       }
-      const bool placeholders = cands.size() > 1;
+      const bool placeholder = n_tiles.size() > 1;
       if (dma) {
-        src << "  static constexpr int BM = " << dm << ", BN = " << (placeholders ? "ACCY_N_TILE" : std::to_string(dn))
-            << ", STAGES = " << (placeholders ? "ACCY_STAGES" : "4") << ";\n};\n";
+        src << "  static constexpr int BM = " << dm << ", BN = " << (placeholder ? "ACCY_N_TILE" : std::to_string(dn))
+            << ", STAGES = 4;\n};\n";
       } else {
         src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
             << ", WAVES_N = " << WN << ";\n};\n";
       }
       int threads = dma ? 256 : WM * WN * 64;
-      src << "extern \"C\" __global__ void " << (placeholders ? std::string("ACCY_LAUNCH_BOUNDS")
-                                                               : "__launch_bounds__(" + std::to_string(threads) + ")")
-          << " " << nm << "(" << w->params() << ") {\n"
+      src << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << nm << "(" << w->params() << ") {\n"
           << "  accy::gemm::" << (dma ? "mma16_dma" : "mma16") << "<Cfg_" << nm << ">(" << a << " + " << gs.a.offset
           << "L, " << b << " + " << gs.b.offset << "L, Epi_" << nm << "{" << inits.str() << "});\n}\n";
       k.source = src.str();
-      if (placeholders) {
+      if (placeholder) {
         k.tuning_key = tuning_key("gemm", k.source, "m=" + std::to_string(gs.m) + ",n=" + std::to_string(gs.n) +
                                                         ",k=" + std::to_string(gs.k) + ",batch=" + std::to_string(gs.batch));
-        k.candidate_count = (uint32_t)cands.size();
+        k.candidate_count = (uint32_t)n_tiles.size();
         k.candidate = candidate_for(k.tuning_key, k.candidate_count);
-        const DmaCandidate& c = cands[k.candidate];
-        dn = c.bn;
-        auto put = [&](const std::string& mark, const std::string& text) {
-          k.source.replace(k.source.find(mark), mark.size(), text);
-        };
-        put("ACCY_N_TILE", std::to_string(c.bn));
-        put("ACCY_STAGES", std::to_string(c.stages));
-        put("ACCY_LAUNCH_BOUNDS", "__launch_bounds__(" + std::to_string(threads) +
-                                      (c.occupancy > 1 ? ", " + std::to_string(c.occupancy) : "") + ")");
+        dn = n_tiles[k.candidate];
+        const std::string mark = "ACCY_N_TILE";
+        k.source.replace(k.source.find(mark), mark.size(), std::to_string(dn));
       }
       int64_t tiles = dma ? ((gs.m + dm - 1) / dm) * ((gs.n + dn - 1) / dn) : ((gs.m + BM - 1) / BM) * ((gs.n + BN - 1) / BN);
       k.grid[0] = (uint32_t)tiles;

@@ -968,6 +968,7 @@ class Planner {
       if (a != r) outer *= t.dims[a].extent;
     if (outer > 65535) return false;
     const int64_t er = t.dims[r].extent, ec = t.dims[n - 1].extent, tc = (ec + 63) / 64;
+    if (((er + 63) / 64) * tc >= (int64_t)1 << 24) return false;  // a launch holds fewer than 2^32 work items
     KernelWriter w(g_, slots_, "i64_t");
     const std::string src = w.arg(pv.slot, false), dst = w.arg(slot, true);
     const std::string T = storage_type(t.dtype);
@@ -1255,6 +1256,7 @@ class Planner {
     if (d != DType::bf16 && d != DType::f16 && d != DType::f32) return false;
     if (!gemm_shape(op, gs)) return false;
     if (gs.m * gs.n * gs.k == 0) return false;
+    if (gs.batch > 65535) return false;  // the batch index is gridDim.y, at most 65535 on gfx950
     if (d == DType::f32) {
       // The f32 MFMA kernel: 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with 16-byte
       // aligned rows. Exact tiles, or M / N off the tile grid (N a multiple of 4) when the problem is

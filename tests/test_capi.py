@@ -94,6 +94,16 @@ def test_small_or_ragged_f32_contractions_keep_serial_order():
         assert "accy::gemm::" not in src
 
 
+def test_contractions_with_more_batches_than_the_grid_holds_take_the_dot():
+    # the matrix-core kernels index the batch by blockIdx.y, at most 65535 on gfx950
+    def batched(dtype, nb):
+        return T.define("bb", [T.spec(dtype, b=nb, m=128, k=128), T.spec(dtype, b=nb, k=128, n=128)],
+                        lambda b, a: a[0].contract(a[1], "k"))
+    assert "accy::gemm::mma16_dma<" in hip.plan_source(batched("bf16", 65535), compile=False)
+    src = hip.plan_source(batched("bf16", 65536), compile=False)
+    assert "accy::gemm::" not in src and "// dot:" in src
+
+
 def test_operands_sharing_one_buffer_compile():
     # x . x^T on the matrix cores and self-attention with q = k = v: one kernel parameter each
     gram = T.define("gram", [T.spec("bf16", m=256, k=128)],

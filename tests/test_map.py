@@ -71,6 +71,9 @@ def test_transposes_are_copied_through_lds_tiles():
     # the innermost axis contiguous in the source already: the vector map
     p = T.define("same", [T.spec("f32", a=4, b=64, c=128)], lambda b, a: b.transpose(a[0], [1, 0, 2]))
     assert "// permute:" not in hip.plan_source(p)
+    # 2^24 tiles of 256 threads would pass 2^32 work items in one launch: the grid-strided map
+    p = T.define("huge", [T.spec("u8", r=1 << 18, c=1 << 18)], lambda b, a: b.transpose(a[0], [1, 0]))
+    assert "// permute:" not in hip.plan_source(p) and "// map:" in hip.plan_source(p)
 
 
 @pytest.mark.gpu

@@ -72,6 +72,44 @@ uint32_t grid_for(uint64_t work_items, uint32_t block, uint64_t cap = 1u << 20) 
   return (uint32_t)std::min<uint64_t>(g, cap);
 }
 
+// The body of a 64 x 64 tile of a transposing copy through LDS, for a kernel that has defined
+// `const long r0, c0` (the tile's first r and c). The source's r axis is contiguous (element (r, c)
+// at src[r + c * sc]), the destination's c axis (element (r, c) at dst[r * ds + c]); extents R and
+// C. Tiles are read along r and written along c, so both sides touch whole lines. `et` is the
+// element's storage type. With `vec4` (R, C, sc and ds multiples of 4 and both bases 4-element
+// aligned), each lane moves 4 elements per access; the LDS row pitch of 65 elements keeps the 64
+// lanes of a wave on distinct banks on both sides.
+std::string transpose_tile(const std::string& et, int64_t R, int64_t C, int64_t sc, int64_t ds, const std::string& src,
+                           const std::string& dst, bool vec4) {
+  std::ostringstream k;
+  const std::string r = std::to_string(R) + "L", c = std::to_string(C) + "L";
+  k << "  __shared__ " << et << " tile[64][65];\n";
+  if (vec4) {
+    k << "  typedef " << et << " V __attribute__((ext_vector_type(4)));\n"
+      << "  const int t = (threadIdx.x & 15) * 4, q = threadIdx.x >> 4;\n"
+      << "  for (int c = q; c < 64; c += 16)\n"
+      << "    if (r0 + t < " << r << " && c0 + c < " << c << ") {\n"
+      << "      const V v = *(const V*)&" << src << "[r0 + t + (c0 + c) * " << sc << "L];\n"
+      << "      tile[c][t] = v.x; tile[c][t + 1] = v.y; tile[c][t + 2] = v.z; tile[c][t + 3] = v.w;\n"
+      << "    }\n"
+      << "  __syncthreads();\n"
+      << "  for (int r = q; r < 64; r += 16)\n"
+      << "    if (r0 + r < " << r << " && c0 + t < " << c << ") {\n"
+      << "      const V v = {tile[t][r], tile[t + 1][r], tile[t + 2][r], tile[t + 3][r]};\n"
+      << "      *(V*)&" << dst << "[(r0 + r) * " << ds << "L + c0 + t] = v;\n"
+      << "    }\n";
+  } else {
+    k << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
+      << "  for (int c = q; c < 64; c += 4)\n"
+      << "    if (r0 + t < " << r << " && c0 + c < " << c << ") tile[c][t] = " << src << "[r0 + t + (c0 + c) * " << sc
+      << "L];\n"
+      << "  __syncthreads();\n"
+      << "  for (int r = q; r < 64; r += 4)\n"
+      << "    if (r0 + r < " << r << " && c0 + t < " << c << ") " << dst << "[(r0 + r) * " << ds << "L + c0 + t] = tile[t][r];\n";
+  }
+  return k.str();
+}
+
 const char* reducer_op(Reducer r) {
   switch (r) {
     case Reducer::sum: return "accy::SumOp()";
@@ -975,23 +1013,16 @@ class Planner {
     std::ostringstream k;
     const std::string nm = name("permute", v);
     k << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << w.params() << ") {\n"
-      << "  __shared__ " << T << " tile[64][65];\n"
       << "  long o = blockIdx.y, so = " << pv.offset << "L, dof = 0;\n";
     for (size_t a = n - 1; a-- > 0;) {
       if (a == r) continue;
       k << "  { const long x = o % " << t.dims[a].extent << "L; o /= " << t.dims[a].extent << "L; so += x * "
         << pv.strides[a] << "L; dof += x * " << ds[a] << "L; }\n";
     }
+    bool vec4 = er % 4 == 0 && ec % 4 == 0 && sc % 4 == 0 && pv.offset % 4 == 0;
+    for (size_t a = 0; a + 1 < n; ++a) vec4 = vec4 && (a == r || pv.strides[a] % 4 == 0) && ds[a] % 4 == 0;
     k << "  const long r0 = (long)(blockIdx.x / " << tc << ") * 64, c0 = (long)(blockIdx.x % " << tc << ") * 64;\n"
-      << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
-      << "  for (int c = q; c < 64; c += 4)\n"
-      << "    if (r0 + t < " << er << "L && c0 + c < " << ec << "L) tile[c][t] = " << src << "[so + r0 + t + (c0 + c) * " << sc
-      << "L];\n"
-      << "  __syncthreads();\n"
-      << "  for (int r = q; r < 64; r += 4)\n"
-      << "    if (r0 + r < " << er << "L && c0 + t < " << ec << "L) " << dst << "[dof + (r0 + r) * " << ds[r]
-      << "L + c0 + t] = tile[t][r];\n"
-      << "}\n";
+      << transpose_tile(T, er, ec, sc, ds[r], "(" + src + " + so)", "(" + dst + " + dof)", vec4) << "}\n";
     KernelStep ks;
     ks.source = k.str();
     ks.name = nm;
@@ -1196,13 +1227,8 @@ class Planner {
       << "  const float* __restrict__ s = " << src << " + " << off << "L + b * " << sb << "L;\n"
       << "  float* __restrict__ d = " << out << " + b * " << R * C << "L;\n";
     if (sr == 1) {
-      k << "  __shared__ float tile[64][65];\n"
-        << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
-        << "  for (int c = q; c < 64; c += 4)\n"
-        << "    if (r0 + t < " << R << "L && c0 + c < " << C << "L) tile[c][t] = s[(r0 + t) + (c0 + c) * " << sc << "L];\n"
-        << "  __syncthreads();\n"
-        << "  for (int r = q; r < 64; r += 4)\n"
-        << "    if (r0 + r < " << R << "L && c0 + t < " << C << "L) d[(r0 + r) * " << C << "L + c0 + t] = tile[t][r];\n";
+      const bool vec4 = R % 4 == 0 && C % 4 == 0 && sc % 4 == 0 && sb % 4 == 0 && off % 4 == 0;
+      k << transpose_tile("float", R, C, sc, C, "s", "d", vec4);
     } else {
       k << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
         << "  for (int r = q; r < 64; r += 4)\n"

@@ -68,6 +68,10 @@ def test_transposes_are_copied_through_lds_tiles():
     p = T.define("tr", [T.spec("f32", r=256, c=512)], lambda b, a: b.transpose(a[0], [1, 0]))
     src = hip.plan_source(p, compile=True)
     assert "// permute:" in src and "tile[64][65]" in src
+    assert "ext_vector_type(4)" in src           # extents and strides multiples of 4: 4 elements per access
+    p = T.define("odd", [T.spec("f32", r=256, c=510)], lambda b, a: b.transpose(a[0], [1, 0]))
+    src = hip.plan_source(p, compile=True)
+    assert "// permute:" in src and "ext_vector_type" not in src
     # the innermost axis contiguous in the source already: the vector map
     p = T.define("same", [T.spec("f32", a=4, b=64, c=128)], lambda b, a: b.transpose(a[0], [1, 0, 2]))
     assert "// permute:" not in hip.plan_source(p)
@@ -83,6 +87,9 @@ def test_transposes_are_copied_through_lds_tiles():
     ("f64", (("a", 3), ("b", 65), ("c", 70)), (0, 2, 1)),
     ("i32", (("a", 2), ("b", 3), ("c", 100), ("d", 64)), (3, 1, 0, 2)),
     ("i1", (("r", 77), ("c", 129)), (1, 0)),
+    ("u8", (("r", 516), ("c", 260)), (1, 0)),
+    ("bf16", (("r", 100), ("c", 4096)), (1, 0)),
+    ("f64", (("a", 2), ("b", 128), ("c", 68)), (0, 2, 1)),
 ])
 def test_transposes_bit_exact(dtype, dims, perm):
     p = T.define("perm", [T.spec(dtype, *dims)], lambda b, a: b.transpose(a[0], list(perm)))
@@ -92,6 +99,8 @@ def test_transposes_bit_exact(dtype, dims, perm):
         x = W.to_dtype(rng.standard_normal(shape), "bf16")
     elif dtype == "i1":
         x = rng.random(shape) < 0.5
+    elif dtype == "u8":
+        x = rng.integers(0, 256, shape).astype(np.uint8)
     elif dtype == "i32":
         x = rng.integers(-10 ** 9, 10 ** 9, shape).astype(np.int32)
     else:

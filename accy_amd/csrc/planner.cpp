@@ -76,26 +76,28 @@ uint32_t grid_for(uint64_t work_items, uint32_t block, uint64_t cap = 1u << 20) 
 // `const long r0, c0` (the tile's first r and c). The source's r axis is contiguous (element (r, c)
 // at src[r + c * sc]), the destination's c axis (element (r, c) at dst[r * ds + c]); extents R and
 // C. Tiles are read along r and written along c, so both sides touch whole lines. `et` is the
-// element's storage type. With `vec4` (R, C, sc and ds multiples of 4 and both bases 4-element
-// aligned), each lane moves 4 elements per access; the LDS row pitch of 65 elements keeps the 64
-// lanes of a wave on distinct banks on both sides.
+// element's storage type. With `epl` > 1 (4, 8 or 16; R, C, sc and ds multiples of it and both bases
+// aligned to it), each lane moves `epl` consecutive elements per access, 16 bytes for 1- to 4-byte
+// elements; otherwise one element per access.
 std::string transpose_tile(const std::string& et, int64_t R, int64_t C, int64_t sc, int64_t ds, const std::string& src,
-                           const std::string& dst, bool vec4) {
+                           const std::string& dst, int epl) {
   std::ostringstream k;
   const std::string r = std::to_string(R) + "L", c = std::to_string(C) + "L";
   k << "  __shared__ " << et << " tile[64][65];\n";
-  if (vec4) {
-    k << "  typedef " << et << " V __attribute__((ext_vector_type(4)));\n"
-      << "  const int t = (threadIdx.x & 15) * 4, q = threadIdx.x >> 4;\n"
-      << "  for (int c = q; c < 64; c += 16)\n"
+  if (epl > 1) {
+    const int lanes = 64 / epl, step = 256 / lanes;  // lanes per 64 elements of r; columns per pass
+    k << "  typedef " << et << " V __attribute__((ext_vector_type(" << epl << ")));\n"
+      << "  const int t = (threadIdx.x % " << lanes << ") * " << epl << ", q = threadIdx.x / " << lanes << ";\n"
+      << "  for (int c = q; c < 64; c += " << step << ")\n"
       << "    if (r0 + t < " << r << " && c0 + c < " << c << ") {\n"
       << "      const V v = *(const V*)&" << src << "[r0 + t + (c0 + c) * " << sc << "L];\n"
-      << "      tile[c][t] = v.x; tile[c][t + 1] = v.y; tile[c][t + 2] = v.z; tile[c][t + 3] = v.w;\n"
+      << "#pragma unroll\n      for (int j = 0; j < " << epl << "; ++j) tile[c][t + j] = v[j];\n"
       << "    }\n"
       << "  __syncthreads();\n"
-      << "  for (int r = q; r < 64; r += 16)\n"
+      << "  for (int r = q; r < 64; r += " << step << ")\n"
       << "    if (r0 + r < " << r << " && c0 + t < " << c << ") {\n"
-      << "      const V v = {tile[t][r], tile[t + 1][r], tile[t + 2][r], tile[t + 3][r]};\n"
+      << "      V v;\n"
+      << "#pragma unroll\n      for (int j = 0; j < " << epl << "; ++j) v[j] = tile[t + j][r];\n"
       << "      *(V*)&" << dst << "[(r0 + r) * " << ds << "L + c0 + t] = v;\n"
       << "    }\n";
   } else {
@@ -108,6 +110,18 @@ std::string transpose_tile(const std::string& et, int64_t R, int64_t C, int64_t 
       << "    if (r0 + r < " << r << " && c0 + t < " << c << ") " << dst << "[(r0 + r) * " << ds << "L + c0 + t] = tile[t][r];\n";
   }
   return k.str();
+}
+
+// Elements per lane access of a tiled transpose: 16 bytes' worth for elements of at most 4 bytes
+// (4 for 8-byte elements), when every extent, stride and offset in `multiples` is a multiple of it;
+// then 4; else 1.
+int transpose_lanes(size_t elem_bytes, const std::vector<int64_t>& multiples) {
+  for (int e : {std::max<int>(4, (int)(16 / elem_bytes)), 4}) {
+    bool ok = true;
+    for (int64_t x : multiples) ok = ok && x % e == 0;
+    if (ok) return e;
+  }
+  return 1;
 }
 
 const char* reducer_op(Reducer r) {
@@ -1019,10 +1033,14 @@ class Planner {
       k << "  { const long x = o % " << t.dims[a].extent << "L; o /= " << t.dims[a].extent << "L; so += x * "
         << pv.strides[a] << "L; dof += x * " << ds[a] << "L; }\n";
     }
-    bool vec4 = er % 4 == 0 && ec % 4 == 0 && sc % 4 == 0 && pv.offset % 4 == 0;
-    for (size_t a = 0; a + 1 < n; ++a) vec4 = vec4 && (a == r || pv.strides[a] % 4 == 0) && ds[a] % 4 == 0;
+    std::vector<int64_t> multiples = {er, ec, sc, pv.offset};
+    for (size_t a = 0; a + 1 < n; ++a) {
+      if (a != r) multiples.push_back(pv.strides[a]);
+      multiples.push_back(ds[a]);
+    }
+    const int epl = transpose_lanes(dtype_size(t.dtype), multiples);
     k << "  const long r0 = (long)(blockIdx.x / " << tc << ") * 64, c0 = (long)(blockIdx.x % " << tc << ") * 64;\n"
-      << transpose_tile(T, er, ec, sc, ds[r], "(" + src + " + so)", "(" + dst + " + dof)", vec4) << "}\n";
+      << transpose_tile(T, er, ec, sc, ds[r], "(" + src + " + so)", "(" + dst + " + dof)", epl) << "}\n";
     KernelStep ks;
     ks.source = k.str();
     ks.name = nm;
@@ -1227,8 +1245,7 @@ class Planner {
       << "  const float* __restrict__ s = " << src << " + " << off << "L + b * " << sb << "L;\n"
       << "  float* __restrict__ d = " << out << " + b * " << R * C << "L;\n";
     if (sr == 1) {
-      const bool vec4 = R % 4 == 0 && C % 4 == 0 && sc % 4 == 0 && sb % 4 == 0 && off % 4 == 0;
-      k << transpose_tile("float", R, C, sc, C, "s", "d", vec4);
+      k << transpose_tile("float", R, C, sc, C, "s", "d", transpose_lanes(4, {R, C, sc, sb, off}));
     } else {
       k << "  const int t = threadIdx.x & 63, q = threadIdx.x >> 6;\n"
         << "  for (int r = q; r < 64; r += 4)\n"

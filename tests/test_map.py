@@ -69,6 +69,11 @@ def test_transposes_are_copied_through_lds_tiles():
     src = hip.plan_source(p, compile=True)
     assert "// permute:" in src and "tile[64][65]" in src
     assert "ext_vector_type(4)" in src           # extents and strides multiples of 4: 4 elements per access
+    # 16 bytes per lane access for small elements when the extents allow it
+    p = T.define("tr8", [T.spec("u8", r=512, c=272)], lambda b, a: b.transpose(a[0], [1, 0]))
+    assert "ext_vector_type(16)" in hip.plan_source(p, compile=True)
+    p = T.define("tr16", [T.spec("bf16", r=200, c=1000)], lambda b, a: b.transpose(a[0], [1, 0]))
+    assert "ext_vector_type(8)" in hip.plan_source(p, compile=True)
     p = T.define("odd", [T.spec("f32", r=256, c=510)], lambda b, a: b.transpose(a[0], [1, 0]))
     src = hip.plan_source(p, compile=True)
     assert "// permute:" in src and "ext_vector_type" not in src
@@ -90,6 +95,9 @@ def test_transposes_are_copied_through_lds_tiles():
     ("u8", (("r", 516), ("c", 260)), (1, 0)),
     ("bf16", (("r", 100), ("c", 4096)), (1, 0)),
     ("f64", (("a", 2), ("b", 128), ("c", 68)), (0, 2, 1)),
+    ("u8", (("r", 512), ("c", 272)), (1, 0)),                 # 16 per lane access, ragged tiles
+    ("bf16", (("r", 200), ("c", 1000)), (1, 0)),              # 8 per lane access
+    ("bf16", (("a", 3), ("b", 64), ("c", 136)), (0, 2, 1)),
 ])
 def test_transposes_bit_exact(dtype, dims, perm):
     p = T.define("perm", [T.spec(dtype, *dims)], lambda b, a: b.transpose(a[0], list(perm)))

@@ -3,7 +3,8 @@ transposes (aligned binaries), compare / select, and reductions over one or two 
 i32, on extents that are and are not multiples of four. Each program runs on the target and on the
 oracle (the runCpu restatement): integer results bit-exact; f32 results within 1e-5 of the largest
 magnitude of the output (reductions may be associated differently, and the values stay in a moderate
-range: no exp / log, divisions by |x| + 1).
+range: no exp / log, divisions by |x| + 1). The same for random contraction programs (matrix-core
+and serial-k paths) and random scans (two carries, elementwise chains and folds in the body).
 """
 import numpy as np
 import pytest
@@ -140,3 +141,75 @@ def test_random_contraction_programs_match_the_oracle(seed, dtype):
     tol = 1e-3 if dtype == "f32" else 2e-2
     for g, r in zip(got, ref):
         assert_normwise(g, r, tol, dtype, floor=None)
+
+
+def _scan_program(seed, dtype):
+    """A scan over two carries, x [a, b] and s [b], for a random number of steps (0-6): x is updated by
+    a random chain of elementwise operations with s broadcast over a, s by a fold of x over a. Read
+    back: the loop, a projection of s, and a value computed from both after the loop."""
+    rng = np.random.default_rng(2000 + seed)
+    ea, eb = (int(rng.choice([1, 5, 64, 130, 1000])) for _ in range(2))
+    length = int(rng.integers(0, 7))
+    scalar = T.Type(dtype, ())
+    ops = [str(rng.choice(["add_s", "sub_s", "max_s", "min_s", "neg", "half", "abs"])) for _ in range(int(rng.integers(1, 5)))]
+    fold = str(rng.choice(["sum", "max", "min"]))
+
+    def const(bb, v):
+        return bb.full_float(scalar, v) if dtype == "f32" else bb.full("i32", int(v))
+
+    def step(bb, c):
+        x, s = c
+        for op in ops:
+            if op == "add_s":
+                x = x.add(s)
+            elif op == "sub_s":
+                x = x.sub(s)
+            elif op == "max_s":
+                x = x.max(s)
+            elif op == "min_s":
+                x = x.min(s)
+            elif op == "neg":
+                x = x.neg()
+            elif op == "abs":
+                x = x.abs()
+            else:   # keep magnitudes bounded: f32 halves, i32 clamps
+                x = x.mul(const(bb, 0.5)) if dtype == "f32" else x.max(const(bb, -10 ** 6)).min(const(bb, 10 ** 6))
+        r = getattr(x, fold)("a")
+        if dtype == "f32" and fold == "sum":
+            r = r.mul(const(bb, 1.0 / ea))
+        return [x, s.add(r) if fold == "sum" else s.max(r) if fold == "max" else s.min(r)]
+
+    def body(b, a):
+        loop = b.scan(length, [a[0], a[1]], step)
+        s = b.projection(loop, 1)
+        return [loop, s, loop.sum("a").add(s)]
+
+    prog = T.define(f"scan{seed}", [T.spec(dtype, a=ea, b=eb), T.spec(dtype, b=eb)], body)
+    if dtype == "f32":
+        inputs = [rng.standard_normal((ea, eb)).astype(np.float32), rng.standard_normal(eb).astype(np.float32)]
+    else:
+        inputs = [rng.integers(-1000, 1000, (ea, eb)).astype(np.int32), rng.integers(-1000, 1000, eb).astype(np.int32)]
+    return prog, inputs
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_random_scan_programs_plan_and_compile(seed):
+    for dtype in ("f32", "i32"):
+        prog, _ = _scan_program(seed, dtype)
+        assert "// loop " in hip.plan_source(prog, compile=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("dtype", ["f32", "i32"])
+def test_random_scan_programs_match_the_oracle(seed, dtype):
+    prog, inputs = _scan_program(seed, dtype)
+    print(f"scan seed {seed} {dtype}: inputs {[t.shape for t in prog.input_types()]}", flush=True)
+    got, ref = hip_run(prog, inputs), oracle_run(prog, inputs)
+    for i, (g, r) in enumerate(zip(got, ref)):
+        if dtype == "i32":
+            assert np.array_equal(g, r), f"output {i}"
+        else:
+            # f32 sums are associated differently on the target; the carries feed them back each step
+            scale = float(np.abs(r).max()) if r.size else 0.0
+            assert np.all(np.abs(g.astype(np.float64) - r) <= 1e-4 * max(scale, 1e-30)), f"output {i}"

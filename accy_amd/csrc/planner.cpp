@@ -83,6 +83,29 @@ std::string transpose_tile(const std::string& et, int64_t R, int64_t C, int64_t 
                            const std::string& dst, int epl) {
   std::ostringstream k;
   const std::string r = std::to_string(R) + "L", c = std::to_string(C) + "L";
+  if (epl == 8) {
+    // 2-byte elements: an LDS word holds the elements of columns 2p and 2p + 1 at one r (the lower
+    // column in the low half, as in memory), so each LDS access moves two elements. A lane loads 8
+    // r of two adjacent columns and writes 8 words; on the way out it reads 4 words of one r (8
+    // consecutive c) for one 16-byte store. Pitch 33 words.
+    k << "  __shared__ u32_t tile[64][33];\n"
+      << "  typedef " << et << " V __attribute__((ext_vector_type(8)));\n"
+      << "  typedef u32_t W __attribute__((ext_vector_type(4)));\n"
+      << "  const int t = (threadIdx.x & 7) * 8, p = threadIdx.x >> 3;\n"
+      << "  if (r0 + t < " << r << " && c0 + 2 * p < " << c << ") {\n"
+      << "    const V a = *(const V*)&" << src << "[r0 + t + (c0 + 2 * p) * " << sc << "L];\n"
+      << "    const V b = *(const V*)&" << src << "[r0 + t + (c0 + 2 * p + 1) * " << sc << "L];\n"
+      << "#pragma unroll\n    for (int j = 0; j < 8; ++j) tile[t + j][p] = (u32_t)(u16_t)a[j] | ((u32_t)(u16_t)b[j] << 16);\n"
+      << "  }\n"
+      << "  __syncthreads();\n"
+      << "  const int w = (threadIdx.x & 7) * 4;\n"
+      << "  for (int r = threadIdx.x >> 3; r < 64; r += 32)\n"
+      << "    if (r0 + r < " << r << " && c0 + 2 * w < " << c << ") {\n"
+      << "      const W v = {tile[r][w], tile[r][w + 1], tile[r][w + 2], tile[r][w + 3]};\n"
+      << "      *(W*)&" << dst << "[(r0 + r) * " << ds << "L + c0 + 2 * w] = v;\n"
+      << "    }\n";
+    return k.str();
+  }
   k << "  __shared__ " << et << " tile[64][65];\n";
   if (epl > 1) {
     const int lanes = 64 / epl, step = 256 / lanes;  // lanes per 64 elements of r; columns per pass

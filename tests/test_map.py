@@ -73,7 +73,7 @@ def test_transposes_are_copied_through_lds_tiles():
     p = T.define("tr8", [T.spec("u8", r=512, c=272)], lambda b, a: b.transpose(a[0], [1, 0]))
     assert "ext_vector_type(16)" in hip.plan_source(p, compile=True)
     p = T.define("tr16", [T.spec("bf16", r=200, c=1000)], lambda b, a: b.transpose(a[0], [1, 0]))
-    assert "ext_vector_type(8)" in hip.plan_source(p, compile=True)
+    assert "ext_vector_type(8)" in hip.plan_source(p, compile=True) and "u32_t tile[64][33]" in hip.plan_source(p)
     p = T.define("odd", [T.spec("f32", r=256, c=510)], lambda b, a: b.transpose(a[0], [1, 0]))
     src = hip.plan_source(p, compile=True)
     assert "// permute:" in src and "ext_vector_type" not in src
@@ -98,6 +98,8 @@ def test_transposes_are_copied_through_lds_tiles():
     ("u8", (("r", 512), ("c", 272)), (1, 0)),                 # 16 per lane access, ragged tiles
     ("bf16", (("r", 200), ("c", 1000)), (1, 0)),              # 8 per lane access
     ("bf16", (("a", 3), ("b", 64), ("c", 136)), (0, 2, 1)),
+    ("i16", (("r", 128), ("c", 72)), (1, 0)),                 # two 16-bit elements per LDS word
+    ("f16", (("a", 2), ("b", 200), ("c", 64)), (2, 0, 1)),
 ])
 def test_transposes_bit_exact(dtype, dims, perm):
     p = T.define("perm", [T.spec(dtype, *dims)], lambda b, a: b.transpose(a[0], list(perm)))
@@ -109,6 +111,8 @@ def test_transposes_bit_exact(dtype, dims, perm):
         x = rng.random(shape) < 0.5
     elif dtype == "u8":
         x = rng.integers(0, 256, shape).astype(np.uint8)
+    elif dtype == "i16":
+        x = rng.integers(-32768, 32768, shape).astype(np.int16)
     elif dtype == "i32":
         x = rng.integers(-10 ** 9, 10 ** 9, shape).astype(np.int32)
     else:

@@ -78,7 +78,8 @@ uint32_t grid_for(uint64_t work_items, uint32_t block, uint64_t cap = 1u << 20) 
 // C. Tiles are read along r and written along c, so both sides touch whole lines. `et` is the
 // element's storage type. With `epl` > 1 (4, 8 or 16; R, C, sc and ds multiples of it and both bases
 // aligned to it), each lane moves `epl` consecutive elements per access, 16 bytes for 1- to 4-byte
-// elements; otherwise one element per access.
+// elements; otherwise one element per access. `epl` comes from transpose_lanes, which gives 8 only
+// for 2-byte elements; the 8 path packs two elements per 32-bit LDS word and assumes that size.
 std::string transpose_tile(const std::string& et, int64_t R, int64_t C, int64_t sc, int64_t ds, const std::string& src,
                            const std::string& dst, int epl) {
   std::ostringstream k;

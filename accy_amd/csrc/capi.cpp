@@ -2,6 +2,7 @@
 // reference session keeps (src/tensor/session/session.zig:99-246), over HIP executors.
 #include "../../include/accy_hip.h"
 
+#include <algorithm>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -22,7 +23,10 @@ thread_local std::string g_last_error;
 struct Entry {
   bool live = false;
   uint32_t generation = 0;
-  std::unique_ptr<Executor> exec;
+  // Shared with every invocation in progress: a release on another thread retires the handle (its
+  // generation moves on, so later calls get INVALID_HANDLE, session.zig:228-233) while an invocation
+  // already running keeps the executor alive until it returns.
+  std::shared_ptr<Executor> exec;
   // Descriptor storage: names and extents per input, then per output.
   std::vector<std::vector<std::string>> names;
   std::vector<std::vector<const char*>> name_ptrs;
@@ -104,10 +108,13 @@ void fill_descriptors(Entry& e) {
   }
 }
 
-bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
-  if (!an || !bn) return false;
-  auto x = (const uint8_t*)a, y = (const uint8_t*)b;
-  return x < y + bn && y < x + an;
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) { return ranges_overlap(a, an, b, bn); }
+
+// The executor of a live handle, held for the duration of a call made outside the table's lock.
+std::shared_ptr<Executor> hold(accy_hip_handle h) {
+  std::lock_guard<std::mutex> lock(g_mu);
+  Entry* e = lookup(h);
+  return e ? e->exec : nullptr;
 }
 
 }  // namespace
@@ -142,7 +149,7 @@ int accy_hip_compile(const uint8_t* wire_bytes, size_t wire_len, accy_hip_handle
     } catch (const Error& e) {
       return fail_with(ACCY_HIP_COMPILE_FAILED, e.what());
     }
-    auto exec = std::make_unique<Executor>(std::move(prog), std::move(plan));
+    auto exec = std::make_shared<Executor>(std::move(prog), std::move(plan));
     std::lock_guard<std::mutex> lock(g_mu);
     Entry* e = &g_entries[index];
     if (e->live) {  // taken by another thread meanwhile
@@ -187,19 +194,16 @@ int accy_hip_describe(accy_hip_handle h, int which, size_t index, accy_hip_descr
   out->names = e->name_ptrs[slot].data();
   out->extents = e->extents[slot].data();
   out->byte_size = t.bytes();
-  out->alignment = (uint32_t)dtype_size(t.dtype);
+  // session.zig:284 reports max(slot alignment, backend minimum): a borrowed device buffer must meet
+  // the 16 bytes accy_hip_invoke_device checks.
+  out->alignment = (uint32_t)std::max<size_t>(dtype_size(t.dtype), kMinBufferAlignment);
   return ACCY_HIP_OK;
 }
 
 int accy_hip_invoke(accy_hip_handle h, const void* const* inputs, const size_t* input_lens, size_t n_inputs,
                     void* const* outputs, const size_t* output_lens, size_t n_outputs) {
-  Executor* ex;
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    Entry* e = lookup(h);
-    if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
-    ex = e->exec.get();
-  }
+  std::shared_ptr<Executor> ex = hold(h);
+  if (!ex) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
   return guarded([&]() -> int {
     if (n_inputs && (!inputs || !input_lens)) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
     if (n_outputs && (!outputs || !output_lens)) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
@@ -219,13 +223,8 @@ int accy_hip_invoke(accy_hip_handle h, const void* const* inputs, const size_t* 
 
 int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t n_inputs, void* const* outputs,
                            size_t n_outputs, void* stream) {
-  Executor* ex;
-  {
-    std::lock_guard<std::mutex> lock(g_mu);
-    Entry* e = lookup(h);
-    if (!e) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
-    ex = e->exec.get();
-  }
+  std::shared_ptr<Executor> ex = hold(h);
+  if (!ex) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
   return guarded([&]() -> int {
     if (n_inputs && !inputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
     if (n_outputs && !outputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
@@ -235,7 +234,7 @@ int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t 
 }
 
 int accy_hip_release(accy_hip_handle h) {
-  std::unique_ptr<Executor> dead;
+  std::shared_ptr<Executor> dead;  // freed here unless an invocation still holds it
   {
     std::lock_guard<std::mutex> lock(g_mu);
     Entry* e = lookup(h);

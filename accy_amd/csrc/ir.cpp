@@ -567,15 +567,6 @@ float f16_bits_to_f32(uint16_t h) {
   return f;
 }
 
-uint16_t f32_to_bf16_rne(float f) {
-  uint32_t x;
-  std::memcpy(&x, &f, 4);
-  if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu)) return (uint16_t)((x >> 16) | 0x40u);
-  uint32_t lsb = (x >> 16) & 1u;
-  x += 0x7fffu + lsb;
-  return (uint16_t)(x >> 16);
-}
-
 uint16_t f32_to_bf16_trunc(float f) {
   uint32_t x;
   std::memcpy(&x, &f, 4);

@@ -200,8 +200,7 @@ std::vector<int64_t> row_major_strides(const std::vector<Dim>& dims);
 bool is_splat_constant(const Op& op);
 uint16_t f32_to_f16_bits(float f);  // round to nearest even
 float f16_bits_to_f32(uint16_t h);
-uint16_t f32_to_bf16_rne(float f);  // round to nearest even (operation results)
-uint16_t f32_to_bf16_trunc(float f);  // Bf16.fromF32 (constant encoding), dtype.zig:6-9
+uint16_t f32_to_bf16_trunc(float f);  // Bf16.fromF32 (constants and operation results), dtype.zig:6-9
 float bf16_bits_to_f32(uint16_t h);
 
 }  // namespace accy

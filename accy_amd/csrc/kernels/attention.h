@@ -108,6 +108,8 @@ __device__ __forceinline__ u32x4 v_frag(const u16_t* lds, int dt, int s, int lan
   return out;
 }
 
+// Probabilities P for the P.V product: an internal operand of the fused kernel (no traced value), packed
+// with the hardware conversion, nearest even for both types.
 template <int DT>
 __device__ __forceinline__ u32_t pack2(float a, float b) {
   typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -118,6 +120,14 @@ __device__ __forceinline__ u32_t pack2(float a, float b) {
     typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
     return __builtin_bit_cast(u32_t, __builtin_convertvector(f32x2{a, b}, h16x2));  // v_cvt_pk_f16_f32 (RNE)
   }
+}
+
+// The output O, a traced result: f16 rounds to nearest even (@floatCast), bf16 keeps the high half of
+// each f32 (Bf16.fromF32, deps/lib/compiler/gpu/abi/src/dtype.zig:6-9), as every bf16 result does.
+template <int DT>
+__device__ __forceinline__ u32_t pack2_out(float a, float b) {
+  if constexpr (DT == 0) return pack_bf16x2(a, b);
+  else return pack2<DT>(a, b);
 }
 
 // max(a, b, c) in one v_max3_f32. (fmaxf on MFMA results costs a canonicalising v_max per value
@@ -473,8 +483,8 @@ struct Accumulator {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x16& acc = o[qt][dt];
-          const u32_t lo = pack2<C::DT>(acc[4 * g] * inv[qt], acc[4 * g + 1] * inv[qt]);
-          const u32_t hi = pack2<C::DT>(acc[4 * g + 2] * inv[qt], acc[4 * g + 3] * inv[qt]);
+          const u32_t lo = pack2_out<C::DT>(acc[4 * g] * inv[qt], acc[4 * g + 1] * inv[qt]);
+          const u32_t hi = pack2_out<C::DT>(acc[4 * g + 2] * inv[qt], acc[4 * g + 3] * inv[qt]);
           *(u32x2*)(orow + dt * 32 + 8 * g + 4 * h) = u32x2{lo, hi};
         }
     }

@@ -22,18 +22,22 @@ typedef unsigned long long u64_t;
 
 namespace accy {
 
-// ---- 16-bit floats: f16 is IEEE binary16, bf16 is the top half of an f32; both round to nearest even.
+// ---- 16-bit floats: f16 is IEEE binary16 and rounds to nearest even (Zig @floatCast); bf16 is the
+// top half of an f32 and every bf16 result keeps the high 16 bits of its f32 value, the reference's
+// Bf16.fromF32 (deps/lib/compiler/gpu/abi/src/dtype.zig:6-9), which its evaluator applies to every
+// bf16 operation result (src/eval/evaluator.zig:2242-2244, 2338, 2384-2386, 2860).
 __device__ __forceinline__ float f16_to_f32(u16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ u16_t f32_to_f16(float x) { return __builtin_bit_cast(u16_t, (_Float16)x); }
 __device__ __forceinline__ float bf16_to_f32(u16_t h) { return __builtin_bit_cast(float, ((u32_t)h) << 16); }
-__device__ __forceinline__ u16_t f32_to_bf16(float x) { return __builtin_bit_cast(u16_t, (__bf16)x); }
+__device__ __forceinline__ u16_t f32_to_bf16(float x) { return (u16_t)(__builtin_bit_cast(u32_t, x) >> 16); }
 __device__ __forceinline__ float round_f16(float x) { return (float)(_Float16)x; }
-// One v_cvt_pk_bf16_f32 of the pair {0, x}: bf16(x) (nearest even) lands in the high half over a
-// zero low half, which is the f32 value of the rounded x, with no shift back.
-typedef float f32x2_rt __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2_rt __attribute__((ext_vector_type(2)));
+// The f32 value of bf16(x): one v_and_b32 of the low mantissa half.
 __device__ __forceinline__ float round_bf16(float x) {
-  return __builtin_bit_cast(float, __builtin_convertvector((f32x2_rt){0.0f, x}, bf16x2_rt));
+  return __builtin_bit_cast(float, __builtin_bit_cast(u32_t, x) & 0xffff0000u);
+}
+// Two bf16 results packed into one word, lo in the low half (the compiler makes it one v_perm_b32).
+__device__ __forceinline__ u32_t pack_bf16x2(float lo, float hi) {
+  return (__builtin_bit_cast(u32_t, lo) >> 16) | (__builtin_bit_cast(u32_t, hi) & 0xffff0000u);
 }
 
 // ---- loads and stores in the compute domain (f32 for 16-bit floats) ----
@@ -174,7 +178,16 @@ __device__ __forceinline__ float cos_f32(float x) {
 template <typename T, typename U> __device__ __forceinline__ T wadd(T a, T b) { return (T)((U)a + (U)b); }
 template <typename T, typename U> __device__ __forceinline__ T wsub(T a, T b) { return (T)((U)a - (U)b); }
 template <typename T, typename U> __device__ __forceinline__ T wmul(T a, T b) { return (T)((U)a * (U)b); }
-template <typename T> __device__ __forceinline__ T idiv(T a, T b) { return b == 0 ? (T)0 : ((b == (T)-1) ? (T)(0 - a) : (T)(a / b)); }
+// Truncating division. A signed division by -1 is a negation that wraps (the most negative value stays
+// itself), computed in 64-bit unsigned arithmetic so no step overflows; unsigned types divide plainly
+// (their all-ones value is a large divisor, not -1).
+template <typename T> __device__ __forceinline__ T idiv(T a, T b) {
+  if (b == 0) return (T)0;
+  if constexpr ((T)-1 < (T)0) {
+    if (b == (T)-1) return (T)(0ull - (u64_t)(i64_t)a);
+  }
+  return (T)(a / b);
+}
 template <typename T> __device__ __forceinline__ T imax(T a, T b) { return a > b ? a : b; }
 template <typename T> __device__ __forceinline__ T imin(T a, T b) { return a < b ? a : b; }
 // A serial fold's float max / min step, as runCpu's x86 code computes it (maxss / minss, then a NaN

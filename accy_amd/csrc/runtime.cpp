@@ -304,6 +304,18 @@ void Executor::invoke_device(const void* const* inputs, size_t n_inputs, void* c
     if (!aligned(inputs[i])) throw HipFailure(kStatusInvalidBuffer, "input " + std::to_string(i) + " not 16-byte aligned");
   for (size_t i = 0; i < n_outputs; ++i)
     if (!aligned(outputs[i])) throw HipFailure(kStatusInvalidBuffer, "output " + std::to_string(i) + " not 16-byte aligned");
+  // binding.zig:325-336 (expectDisjointOutputs): an output may share no byte with an input or with an
+  // earlier output; kernels that read after another workgroup wrote would otherwise see its results.
+  // Inputs may alias each other (they are only read).
+  for (size_t o = 0; o < n_outputs; ++o) {
+    const size_t ob = plan_.slots[(size_t)plan_.output_slots[o]].bytes;
+    for (size_t i = 0; i < n_inputs; ++i)
+      if (ranges_overlap(outputs[o], ob, inputs[i], plan_.slots[(size_t)plan_.input_slots[i]].bytes))
+        throw HipFailure(kStatusInvalidBuffer, "output " + std::to_string(o) + " overlaps input " + std::to_string(i));
+    for (size_t j = 0; j < o; ++j)
+      if (ranges_overlap(outputs[o], ob, outputs[j], plan_.slots[(size_t)plan_.output_slots[j]].bytes))
+        throw HipFailure(kStatusInvalidBuffer, "output " + std::to_string(o) + " overlaps output " + std::to_string(j));
+  }
   for (size_t i = 0; i < n_inputs; ++i) bound_[(size_t)plan_.input_slots[i]] = const_cast<void*>(inputs[i]);
   for (size_t i = 0; i < n_outputs; ++i) bound_[(size_t)plan_.output_slots[i]] = outputs[i];
   run_steps(stream);

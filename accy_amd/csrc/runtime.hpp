@@ -28,6 +28,13 @@ constexpr int kStatusOk = 0, kStatusInvalidProgram = 1, kStatusUnsupportedVersio
 // Device buffers passed in place must be aligned to this many bytes (hipMalloc's are).
 constexpr uintptr_t kMinBufferAlignment = 16;
 
+// True when the byte ranges [a, a + an) and [b, b + bn) share a byte (empty ranges share none).
+inline bool ranges_overlap(const void* a, size_t an, const void* b, size_t bn) {
+  if (!an || !bn) return false;
+  auto x = (const uint8_t*)a, y = (const uint8_t*)b;
+  return x < y + bn && y < x + an;
+}
+
 // Compiles one generated kernel source for gfx950 with hiprtc; returns the code object.
 std::vector<char> compile_kernel_source(const std::string& source, const std::string& name);
 

@@ -27,10 +27,11 @@ from . import tensor as T
 MASK64 = (1 << 64) - 1
 
 
-def splitmix64(seed: int, n: int) -> np.ndarray:
-    """n consecutive SplitMix64 outputs (uint64) from ``seed`` (vectorised)."""
+def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """SplitMix64 outputs number start + 1 .. start + n (uint64) of the stream from ``seed``
+    (vectorised; the stream is counter-based, so any window can be computed on its own)."""
     gamma = np.uint64(0x9E3779B97F4A7C15)
-    idx = np.arange(1, n + 1, dtype=np.uint64)
+    idx = np.arange(start + 1, start + n + 1, dtype=np.uint64)
     with np.errstate(over="ignore"):
         z = np.uint64(seed & MASK64) + idx * gamma
         z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
@@ -45,17 +46,50 @@ def uniform(seed: int, n: int, lo: float, hi: float) -> np.ndarray:
     return lo + (hi - lo) * u
 
 
-def normal(seed: int, n: int) -> np.ndarray:
-    """f64 standard normals, Box-Muller over pairs of uniforms in (0, 1]."""
-    m = (n + 1) // 2
-    u = (splitmix64(seed, 2 * m) >> np.uint64(40)).astype(np.float64)
+def _normal_pairs(seed: int, first_pair: int, pairs: int) -> np.ndarray:
+    """Box-Muller values 2 first_pair .. 2 (first_pair + pairs) - 1 of the stream (f64)."""
+    u = (splitmix64(seed, 2 * pairs, 2 * first_pair) >> np.uint64(40)).astype(np.float64)
     u1 = (u[0::2] + 1.0) * (1.0 / (1 << 24))
     u2 = u[1::2] * (1.0 / (1 << 24))
     r = np.sqrt(-2.0 * np.log(u1))
-    z = np.empty(2 * m)
+    z = np.empty(2 * pairs)
     z[0::2] = r * np.cos(2 * math.pi * u2)
     z[1::2] = r * np.sin(2 * math.pi * u2)
-    return z[:n]
+    return z
+
+
+def normal(seed: int, n: int) -> np.ndarray:
+    """f64 standard normals, Box-Muller over pairs of uniforms in (0, 1]."""
+    return _normal_pairs(seed, 0, (n + 1) // 2)[:n]
+
+
+_CHUNK_PAIRS = 1 << 20
+
+
+def normal_as(seed: int, n: int, dtype: str, scale: float = 1.0) -> np.ndarray:
+    """``to_dtype(normal(seed, n) * scale, dtype)``, the same bytes, generated in chunks of 2^21 values
+    so that the f64 temporaries stay in cache (a 2^28-value tensor takes seconds, not a minute)."""
+    m = (n + 1) // 2
+    out = np.empty(n, to_dtype(np.zeros(0), dtype).dtype)
+
+    def fill(p0: int) -> None:
+        pairs = min(_CHUNK_PAIRS, m - p0)
+        z = _normal_pairs(seed, p0, pairs)
+        if scale != 1.0:
+            z = z * scale
+        part = to_dtype(z[: min(2 * pairs, n - 2 * p0)], dtype)
+        out[2 * p0: 2 * p0 + part.size] = part
+
+    starts = range(0, m, _CHUNK_PAIRS)
+    if len(starts) > 1:
+        # numpy releases the interpreter lock inside its array operations, so chunks run in parallel
+        from concurrent.futures import ThreadPoolExecutor
+        with ThreadPoolExecutor(max_workers=min(8, len(starts))) as pool:
+            list(pool.map(fill, starts))
+    else:
+        for p0 in starts:
+            fill(p0)
+    return out
 
 
 def to_dtype(x: np.ndarray, dtype: str) -> np.ndarray:
@@ -149,7 +183,7 @@ def logsumexp_program(rows: int = 32768, features: int = 8192, dtype: str = "f32
 
 
 def logsumexp_inputs(rows: int = 32768, features: int = 8192, seed: int = 2, dtype: str = "f32") -> List[np.ndarray]:
-    return [to_dtype(normal(seed, rows * features), dtype).reshape(rows, features)]
+    return [normal_as(seed, rows * features, dtype).reshape(rows, features)]
 
 
 # ---------------------------------------------------------------------------------------------
@@ -205,7 +239,7 @@ def attention_program(heads: int = 32, seq: int = 4096, dim: int = 128, dtype: s
 
 def attention_inputs(heads: int = 32, seq: int = 4096, dim: int = 128, dtype: str = "f16", seed: int = 4) -> List[np.ndarray]:
     n = heads * seq * dim
-    return [to_dtype(normal(seed + 100 * i, n), dtype).reshape(heads, seq, dim) for i in range(3)]
+    return [normal_as(seed + 100 * i, n, dtype).reshape(heads, seq, dim) for i in range(3)]
 
 
 # ---------------------------------------------------------------------------------------------
@@ -261,7 +295,7 @@ def decoder_program(batch: int = 4, seq: int = 2048, model: int = 2048, heads: i
 def decoder_inputs(batch: int = 4, seq: int = 2048, model: int = 2048, heads: int = 16, hd: int = 128,
                    ffn: int = 8192, dtype: str = "bf16", seed: int = 5) -> List[np.ndarray]:
     def w(i, *shape, std=0.02):
-        return to_dtype(std * normal(seed + 100 * i, int(np.prod(shape))), dtype).reshape(shape)
+        return normal_as(seed + 100 * i, int(np.prod(shape)), dtype, std).reshape(shape)
     ones = lambda n: to_dtype(np.ones(n), dtype)
     return [w(0, batch, seq, model, std=1.0), ones(model), w(1, model, heads, hd), w(2, model, heads, hd),
             w(3, model, heads, hd), w(4, heads, hd, model), ones(model), w(5, model, ffn), w(6, ffn, model)]

@@ -1,6 +1,6 @@
 """Benchmark of the MI355X execution target on the reference's measured configurations.
 
-``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2-lse]`` prints ONE JSON line.
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--config all]`` prints ONE JSON line.
 
 * A step is one launch of the compiled program (``Hip.launch_device``) over inputs already resident
   in HBM, on one HIP stream; K steps are timed between two synchronisations.
@@ -15,8 +15,11 @@
 * ``cpu_baseline`` is the CPU oracle (the runCpu restatement, oracle/) timed on this host on a
   bounded sample of the same workload, then scaled to the metric's unit (kind "port").
 
-The default workload is C2 (row-wise logsumexp, x f32[32768, 8192]), the configuration the metric
-is quoted on that fits one GPU. Other configs are parity cases; ``--config`` measures them too.
+The headline workload is C2 (row-wise logsumexp, x f32[32768, 8192]), the configuration the metric
+is quoted on that fits one GPU: ``value``, ``roofline`` and ``cpu_baseline`` are C2's. The default run
+(``--config all``) measures every config in the same process and adds ``configs``: per config the step
+time, throughput, the dominant kernel's roofline fraction and HBM traffic, and a bounded CPU baseline.
+``--config NAME`` measures one config alone (its line then has no ``configs``).
 """
 from __future__ import annotations
 
@@ -137,16 +140,21 @@ def config_table():
     }
 
 
-def oracle_time(cfg, budget_s: float = 8.0):
-    """Times the CPU oracle on the config's bounded sample, with all host threads (capped at 16) and
-    with one thread (runCpu launches single-threaded); each until `budget_s` is spent (at most 50
-    runs; about 16 s of CPU work in all). The oracle's per-output order makes both bit-identical."""
+def cpu_threads() -> int:
+    """Host threads for the CPU legs: $ACCY_CPU_THREADS, else the host's cores capped at 16 (the CPU
+    share of one GPU on the measurement boxes)."""
+    return min(int(os.environ.get("ACCY_CPU_THREADS", "0")) or (os.cpu_count() or 1), 16)
+
+
+def oracle_time(cfg, budget_s: float):
+    """Times the CPU oracle on the config's bounded sample, with all host threads and with one thread
+    (runCpu launches single-threaded); each leg until `budget_s` is spent (at most 50 runs). The
+    oracle's per-output order makes both legs bit-identical."""
     sys.path.insert(0, str(ROOT / "tests"))
     from conftest import oracle_lib, oracle_run
     prog, ins, work = cfg["sample"]()
     lib = oracle_lib()
-    threads = int(os.environ.get("ACCY_CPU_THREADS", "0")) or (os.cpu_count() or 1)
-    threads = min(threads, 16)
+    threads = cpu_threads()
     scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
 
     def timed(n):
@@ -170,20 +178,10 @@ def oracle_time(cfg, budget_s: float = 8.0):
                                  sample=f"median of {n_one} runs, {t_one:.3f} s each"))
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", default="c2-lse")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (asked for {args.gpus}); the target runs on a single MI355X "
-              "and has no multi-GPU path.", file=sys.stderr)
-        return 2
-    cfgs = config_table()
-    cfg = cfgs[args.config]
+def measure(name: str, cfg: dict, steps: int, warmup: int) -> dict:
+    """Runs one config on the GPU: K timed steps over HBM-resident inputs, then K profiled steps for
+    the per-kernel durations. Returns the step time, the throughput and the dominant kernel's
+    roofline entry."""
     prog, ins = cfg["make"]()
     # Inputs are copied into HBM before the timed region; outputs stay on the device.
     dins = [hip.DeviceBuffer.from_array(x) for x in ins]
@@ -197,24 +195,24 @@ def main() -> int:
     def step():
         ex.launch_device(iptr, optr, stream.handle)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     stream.synchronize()
     start, end = hip.Event(), hip.Event()
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     end.record(stream)
     stream.synchronize()
     elapsed = time.perf_counter() - t0
-    event_ms = start.elapsed_ms(end) / args.steps
-    ms_per_step = max(elapsed * 1e3 / args.steps, event_ms)
+    event_ms = start.elapsed_ms(end) / steps
+    ms_per_step = max(elapsed * 1e3 / steps, event_ms)
 
     # Per-kernel durations: HIP events recorded on the launch stream around each kernel, over the
     # same number of back-to-back steps (no synchronisation between them).
     ex.set_profiling(True)
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     per_kernel = {k.label: k for k in ex.kernels()}
     ex.set_profiling(False)
@@ -222,39 +220,82 @@ def main() -> int:
     dom_stats = dominant[1]
     # A one-kernel program's kernel duration is the events around the timed region over the steps
     # (events around each launch add a few microseconds each); several kernels need their own events.
-    dom_ms = event_ms if len(per_kernel) == 1 else float(dom_stats.mean_ms)
+    single = len(per_kernel) == 1
+    dom_ms = event_ms if single else float(dom_stats.mean_ms)
     scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
     value = cfg["work"] / (ms_per_step * 1e-3) / scale
     # The roofline is the dominant kernel's: a one-kernel program's work is the config's; in a
     # program of several kernels it is that kernel's own algorithmic bytes or flops.
-    single = len(per_kernel) == 1
     if cfg["bound"] == "hbm":
         work = cfg["work"] if single else dom_stats.algorithmic_bytes
         achieved = work / (dom_ms * 1e-3) / 1e9
         roof = dict(bound="hbm", achieved=achieved, peak=cfg["peak"], unit="GB/s", frac=achieved / cfg["peak"],
-                    traffic=measured_traffic(args.config, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
+                    traffic=measured_traffic(name, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
     else:
         work = cfg["work"] if single else dom_stats.algorithmic_flops
         achieved = work / (dom_ms * 1e-3) / 1e12
         peak = cfg["peak"] / 1000.0 if cfg["unit"] == "GFLOP/s" else cfg["peak"]
         roof = dict(bound=cfg["bound"], achieved=achieved, peak=peak, unit="TFLOP/s", frac=achieved / peak,
-                    traffic=measured_traffic(args.config, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
-    insts = measured_valu(args.config, dominant[0])
+                    traffic=measured_traffic(name, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
+    insts = measured_valu(name, dominant[0])
     if insts is not None:
         # VALU issue fraction (instructions x 64 lanes per second against 256 CUs x 2.4 GHz x 64)
         roof["valu_issue"] = dict(insts_per_launch=insts, frac=insts / (dom_ms * 1e-3) / VALU_ISSUE_PEAK)
-    cpu = None if args.no_cpu else oracle_time(cfg)
-    line = {
-        "metric": METRIC, "value": value, "unit": cfg["unit"], "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": cfg["dtype"], "data": "synthetic (seeded SplitMix64)",
-        "config": dict(workload=args.config, **cfg["workload"]),
-        "roofline": roof, "cpu_baseline": cpu,
-        "kernels": {lbl: float(k.mean_ms) for lbl, k in per_kernel.items()},
-    }
     ex.deinit()
     for b in dins + douts:
         b.free()
+    stream.destroy()
+    return dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"],
+                workload=dict(workload=name, **cfg["workload"]), roofline=roof,
+                kernels={lbl: float(k.mean_ms) for lbl, k in per_kernel.items()})
+
+
+HEADLINE = "c2-lse"
+ALL = ["c2-lse", "c1-tone", "c3-gemm-f32", "c3-gemm-bf16", "c4-attention", "c5-decoder"]
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="all",
+                    help="'all' (the headline C2 line plus every config under 'configs') or one config")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--cpu-budget", type=float, default=6.0,
+                    help="seconds per CPU leg for the headline config (the other configs get a third)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for {args.gpus}); the target runs on a single MI355X "
+              "and has no multi-GPU path.", file=sys.stderr)
+        return 2
+    cfgs = config_table()
+    names = ALL if args.config == "all" else [args.config]
+    head = HEADLINE if args.config == "all" else args.config
+    results = {}
+    for name in names:
+        print(f"bench: {name}", file=sys.stderr, flush=True)
+        r = measure(name, cfgs[name], args.steps, args.warmup)
+        budget = args.cpu_budget if name == head else args.cpu_budget / 3
+        r["cpu_baseline"] = None if args.no_cpu else oracle_time(cfgs[name], budget)
+        results[name] = r
+    h = results[head]
+    line = {
+        "metric": METRIC, "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": h["dtype"], "data": "synthetic (seeded SplitMix64)",
+        "config": h["workload"], "roofline": h["roofline"], "cpu_baseline": h["cpu_baseline"],
+        "kernels": h["kernels"],
+    }
+    if len(names) > 1:
+        line["configs"] = {
+            n: dict(ms=r["ms_per_step"], value=r["value"], unit=r["unit"], dtype=r["dtype"], bound=r["roofline"]["bound"],
+                    kernel=r["roofline"]["kernel"], kernel_ms=r["roofline"]["kernel_ms"],
+                    achieved=r["roofline"]["achieved"], peak=r["roofline"]["peak"],
+                    roofline_unit=r["roofline"]["unit"], frac=r["roofline"]["frac"],
+                    traffic=r["roofline"]["traffic"], valu_issue=r["roofline"].get("valu_issue"),
+                    cpu_baseline=r["cpu_baseline"], kernels=r["kernels"])
+            for n, r in results.items()}
     print(json.dumps(line), flush=True)
     return 0
 

@@ -7,8 +7,10 @@
  * `tensor.runCpu` (src/tensor/execute.zig:54-63; src/executable/binding.zig:127).
  *
  * Every function returns a status number with the reference session's meanings
- * (src/tensor/session/session.zig:33-43). Calls on one handle are not thread-safe with respect
- * to each other; the handle table itself is locked.
+ * (src/tensor/session/session.zig:33-43). Invocations on one handle are not thread-safe with
+ * respect to each other; the handle table itself is locked, and a release on another thread while
+ * an invocation runs retires the handle (later calls get ACCY_HIP_INVALID_HANDLE) but frees the
+ * program only when that invocation has returned.
  */
 #ifndef ACCY_HIP_H
 #define ACCY_HIP_H
@@ -45,6 +47,8 @@ typedef struct {
 
 /* One input or output (session.zig:66-74). `dtype` uses the wire dtype codes
  * (src/tensor/wire/format.zig:97-99: i1=0 … f16=9, bf16=10, f32=11, f64=12, key=13).
+ * `alignment` is max(element size, 16): the 16-byte minimum accy_hip_invoke_device checks, as the
+ * reference reports max(slot alignment, backend minimum) (session.zig:278-284).
  * `names` and `extents` stay valid until the program is released. */
 typedef struct {
   uint32_t dtype;
@@ -95,8 +99,9 @@ int accy_hip_invoke(accy_hip_handle h, const void* const* inputs, const size_t* 
  * pointers sized by the descriptors, and the work is enqueued on `stream` (a hipStream_t; NULL is
  * the null stream) without synchronising. Borrowed in place as `binding.prepareBorrowed` does
  * (src/executable/binding.zig:138-200), which refuses a slice below the backend's minimum
- * alignment: here 16 bytes (hipMalloc's pointers are 256-byte aligned); a misaligned pointer or a
- * count that does not match returns ACCY_HIP_INVALID_BUFFER before anything is launched. */
+ * alignment: here 16 bytes (hipMalloc's pointers are 256-byte aligned); a misaligned pointer, a
+ * count that does not match, or an output whose descriptor-sized range overlaps an input or an earlier
+ * output (binding.zig:325-336) returns ACCY_HIP_INVALID_BUFFER before anything is launched. */
 int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t n_inputs, void* const* outputs,
                            size_t n_outputs, void* stream);
 

@@ -10,7 +10,11 @@
 //  * dot_general: per output a serial f32 `acc = acc + a*b` over the contracted index, multiply and
 //    add rounded separately (lowering/dot.zig:2049-2115; choir x64 scalar.zig:925-962 emits FMA only
 //    for an explicit fma op) — this file is built with -ffp-contract=off;
-//  * 16-bit floats compute in f32 and round back after every operation (src/eval/root.zig:14-16);
+//  * 16-bit floats compute in f32 and round back after every operation (src/eval/root.zig:14-16):
+//    f16 to nearest even (Zig @floatCast), bf16 by truncation (Bf16.fromF32 keeps the high 16 bits,
+//    deps/lib/compiler/gpu/abi/src/dtype.zig:6-9; used for every bf16 result of the evaluator,
+//    src/eval/evaluator.zig:2242-2244 binary, 2338 unary, 2384-2386 pow, 2860 convert), so
+//    reductions and dots that accumulate bf16 in f32 also truncate at the store;
 //  * sin/cos/tan/exp/log/tanh/pow are libm calls (deps/lib/base/sys/src/math.zig:58-125;
 //    scalar.zig:804-828), sqrt is the correctly rounded sqrt (scalar.zig:736);
 //  * gather clamps indices into [0, extent-1] (lowering/elementwise.zig:1190-1208);
@@ -89,11 +93,12 @@ inline void store_i(Tensor& t, uint64_t i, int64_t v) {
   }
 }
 
-// Rounds a value computed in f32 (or f64 for f64 tensors) into the storage format.
+// Rounds a value computed in f32 (or f64 for f64 tensors) into the storage format: f16 to nearest
+// even (@floatCast), bf16 by truncation (Bf16.fromF32, dtype.zig:6-9; evaluator.zig:2242-2244).
 inline void store_f(Tensor& t, uint64_t i, double v) {
   switch (t.type.dtype) {
     case DType::f16: t.as<uint16_t>()[i] = f32_to_f16_bits((float)v); break;
-    case DType::bf16: t.as<uint16_t>()[i] = f32_to_bf16_rne((float)v); break;
+    case DType::bf16: t.as<uint16_t>()[i] = f32_to_bf16_trunc((float)v); break;
     case DType::f32: t.as<float>()[i] = (float)v; break;
     case DType::f64: t.as<double>()[i] = v; break;
     default: fail(Err::Unsupported);

@@ -562,6 +562,51 @@ def test_16bit_arithmetic_chains_bit_exact(dtype):
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
+def test_bf16_serial_fold_truncates_at_the_store_bit_exact():
+    """A bf16 sum over a leading axis runs as a serial fold in runCpu's order with an f32 accumulator;
+    the stored value keeps the high half of the f32 (Bf16.fromF32, dtype.zig:6-9), bit for bit."""
+    x = W.to_dtype(W.normal(31, 96 * 512).reshape(96, 512), "bf16")
+    prog = T.define("s", [T.spec("bf16", k=96, n=512)], lambda b, a: a[0].sum("k"))
+    got, ref = hip_run(prog, [x])[0], oracle_run(prog, [x])[0]
+    assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("dtype,top", [("u8", 2 ** 8 - 1), ("u16", 2 ** 16 - 1), ("u32", 2 ** 32 - 1),
+                                       ("u64", 2 ** 64 - 1), ("i32", -1), ("i64", -1)])
+def test_integer_division_by_the_all_ones_value_exact(dtype, top):
+    """Unsigned x / max is plain division (0, or 1 at max); signed x / -1 wraps (the most negative
+    value stays itself). Bit-exact with the oracle."""
+    npd = {"u8": np.uint8, "u16": np.uint16, "u32": np.uint32, "u64": np.uint64, "i32": np.int32,
+           "i64": np.int64}[dtype]
+    info = np.iinfo(npd)
+    x = np.array([5, 0, info.max, info.max - 1, 1, info.max // 2, info.min, 7], npd)
+    y = np.array([top] * 8, dtype=np.int64 if top < 0 else np.uint64).astype(npd)
+    prog = T.define("d", [T.spec(dtype, i=8)] * 2, lambda b, a: a[0].div(a[1]))
+    got, ref = hip_run(prog, [x, y])[0], oracle_run(prog, [x, y])[0]
+    assert np.array_equal(got, ref), (got, ref)
+
+
+def test_device_tan_and_pow_against_float64():
+    """tan and pow (OCML on the device): within 4 ulp of the float64 value of the f32 arguments, and
+    pow's special cases (x^0 = 1, 1^y = 1, (-2)^3 = -8, (-2)^0.5 = NaN, 0^-1 = inf, (-8)^2 = 64)."""
+    rng = np.random.default_rng(15)
+    x = np.concatenate([rng.uniform(-1.5, 1.5, 20000), rng.uniform(-100, 100, 20000)]).astype(np.float32)
+    got = hip_run(T.define("t", [T.spec("f32", i=len(x))], lambda b, a: a[0].tan()), [x])[0]
+    err = _ulp_error(got, np.tan(x.astype(np.float64)))
+    assert err.max() <= 4.0, f"tan: worst {err.max():.2f} ulp at x = {x[err.argmax()]!r}"
+    base = np.concatenate([rng.uniform(0.05, 20, 30000), [2.0, 1.0, -2.0, -2.0, 0.0, -8.0, 3.0]]).astype(np.float32)
+    expo = np.concatenate([rng.uniform(-8, 8, 30000), [0.0, 123.4, 3.0, 0.5, -1.0, 2.0, 0.0]]).astype(np.float32)
+    got = hip_run(T.define("p", [T.spec("f32", i=len(base))] * 2, lambda b, a: a[0].pow(a[1])), [base, expo])[0]
+    with np.errstate(all="ignore"):
+        ref = np.power(base.astype(np.float64), expo.astype(np.float64))
+    fin = np.isfinite(ref) & (np.abs(ref) < 3e38) & (np.abs(ref) > 1e-37)
+    err = _ulp_error(got[fin], ref[fin])
+    assert err.max() <= 4.0, f"pow: worst {err.max():.2f} ulp"
+    tail = got[-7:]
+    assert tail[0] == 1.0 and tail[1] == 1.0 and tail[2] == -8.0 and np.isnan(tail[3])
+    assert tail[4] == np.inf and tail[5] == 64.0 and tail[6] == 1.0
+
+
 def test_integer_compare_select_gather_scatter_exact():
     def body(b, a):
         x, idx, v = a
@@ -629,6 +674,69 @@ def test_table_holds_at_most_64_programs():
     assert e.value.status == hip.TOO_MANY_PROGRAMS
     for h in hs:
         s.release(h)
+
+
+def test_descriptor_alignment_overlap_and_release_during_invoke():
+    """The descriptor's alignment is the 16 bytes accy_hip_invoke_device enforces (session.zig:278-284);
+    on the device path an output overlapping an input or an earlier output is refused before any launch
+    (binding.zig:325-336); a release on another thread while invocations run retires the handle
+    without freeing the program under them (session.zig:228-233)."""
+    import threading
+    # positive terms, so the row kernel's tree order stays within 1e-5 of runCpu's serial sum
+    prog = T.define("two", [T.spec("f32", row=64, feature=4096)],
+                    lambda b, a: [a[0].mul(a[0]).sum("feature"), a[0].max("feature")])
+    x = W.logsumexp_inputs(64, 4096, seed=21)[0]
+    ref = oracle_run(prog, [x])
+    s = hip.Session()
+    h = s.compile(prog)
+    for d in s.input_descriptors(h) + s.output_descriptors(h):
+        assert d.alignment == 16
+    hb = s.compile(T.define("b", [T.spec("bf16", i=8)], lambda b, a: a[0].neg()))
+    assert s.input_descriptors(hb)[0].alignment == 16
+    s.release(hb)
+    dx = hip.DeviceBuffer.from_array(x)
+    douts = hip.DeviceBuffer(2 * 64 * 4)
+    o1, o2 = douts.ptr, douts.ptr + 64 * 4      # adjacent, disjoint
+    stream = hip.Stream()
+    s.invoke_device(h, [dx.ptr], [o1, o2], stream.handle)
+    stream.synchronize()
+    got = np.zeros(128, np.float32)
+    douts.download(got)
+    assert_rel(got[:64], ref[0], 1e-5)
+    assert np.array_equal(got[64:], ref[1])
+    for outs in ([dx.ptr + 4096, o2], [o1, o1 + 16 * 4], [o1, dx.ptr + 64 * 4096 * 4 - 16]):
+        with pytest.raises(hip.HipError) as e:
+            s.invoke_device(h, [dx.ptr], outs, stream.handle)
+        assert e.value.status == hip.INVALID_BUFFER, outs
+    s.invoke_device(h, [dx.ptr], [o2, o1], stream.handle)   # swapped, still disjoint
+    stream.synchronize()
+    douts.download(got)
+    assert np.array_equal(got[:64], ref[1])
+    statuses, wrong = [], []
+
+    def worker():
+        outs = [np.zeros(64, np.float32), np.zeros(64, np.float32)]
+        for _ in range(200):
+            try:
+                s.invoke(h, [x], outs)
+                statuses.append(hip.OK)
+                if not np.array_equal(outs[1], ref[1]):
+                    wrong.append(outs[1].copy())
+            except hip.HipError as e:
+                statuses.append(e.status)
+    t = threading.Thread(target=worker)
+    t.start()
+    while not statuses:
+        pass
+    s.release(h)
+    t.join()
+    assert statuses[0] == hip.OK and set(statuses) <= {hip.OK, hip.INVALID_HANDLE} and not wrong
+    with pytest.raises(hip.HipError) as e:
+        s.invoke(h, [x], [np.zeros(64, np.float32), np.zeros(64, np.float32)])
+    assert e.value.status == hip.INVALID_HANDLE
+    dx.free()
+    douts.free()
+    stream.destroy()
 
 
 def test_executor_launches_many_times_and_device_invoke():

@@ -149,16 +149,90 @@ def test_f16_binary_ops_round_to_nearest_even_after_each_op(op):
         np.nan_to_num(got.astype(np.float32)), np.nan_to_num(ref.astype(np.float32)))
 
 
-def test_bf16_ops_round_to_nearest_even():
+def _bf16_trunc(x32):
+    """Bf16.fromF32 (deps/lib/compiler/gpu/abi/src/dtype.zig:6-9): the high 16 bits of the f32."""
+    return (np.asarray(x32, np.float32).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+
+
+def _bf16_rne(x32):
+    b = np.asarray(x32, np.float32).view(np.uint32).astype(np.uint64)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_bf16_ops_truncate():
+    """Every bf16 operation result keeps the high half of its f32 value (Bf16.fromF32, applied by the
+    reference evaluator to binary ops at src/eval/evaluator.zig:2242-2244, unary at :2338, pow at
+    :2384-2386, converts at :2860), not the nearest even. The inputs are chosen so that about half of
+    the f32 results round up under nearest even: a nearest-even oracle fails every check."""
     rng = np.random.default_rng(4)
     a32 = rng.standard_normal(2048).astype(np.float32)
     b32 = rng.standard_normal(2048).astype(np.float32)
     a, b = W.to_dtype(a32, "bf16"), W.to_dtype(b32, "bf16")
-    prog = T.define("e", [T.spec("bf16", i=2048), T.spec("bf16", i=2048)], lambda bb, x: x[0].mul(x[1]))
-    got = oracle_run(prog, [a, b])[0]
-    exact = W.bf16_to_f32(a).astype(np.float64) * W.bf16_to_f32(b).astype(np.float64)
-    ref = W.to_dtype(exact.astype(np.float32), "bf16")   # product exact in f32, then RNE to bf16
-    assert np.array_equal(got, ref)
+    fa, fb = W.bf16_to_f32(a), W.bf16_to_f32(b)
+    prog = T.define("e", [T.spec("bf16", i=2048), T.spec("bf16", i=2048)],
+                    lambda bb, x: [x[0].mul(x[1]), x[0].add(x[1]), x[0].exp(), x[0].abs().pow(x[1])])
+    mul, add, ex, pw = oracle_run(prog, [a, b])
+    prod = (fa.astype(np.float64) * fb.astype(np.float64)).astype(np.float32)   # exact in f32
+    summ = (fa.astype(np.float64) + fb.astype(np.float64)).astype(np.float32)   # exact in f32
+    for got, f32 in [(mul, prod), (add, summ), (ex, np.exp(fa)), (pw, np.power(np.abs(fa), fb))]:
+        assert np.array_equal(got, _bf16_trunc(f32))
+        assert (got != _bf16_rne(f32)).mean() > 0.2
+
+
+def test_bf16_reduction_and_dot_truncate_at_the_store():
+    """A bf16 sum and a bf16 contraction accumulate in f32 (reduction.zig:847, 861; dot.zig:2004,
+    2015) and the stored result is Bf16.fromF32 of the f32 accumulator: truncated."""
+    rng = np.random.default_rng(14)
+    x = W.to_dtype(rng.standard_normal((64, 96)).astype(np.float32), "bf16")
+    y = W.to_dtype(rng.standard_normal((96, 32)).astype(np.float32), "bf16")
+    fx, fy = W.bf16_to_f32(x), W.bf16_to_f32(y)
+    prog = T.define("r", [T.spec("bf16", m=64, k=96), T.spec("bf16", k=96, n=32)],
+                    lambda bb, a: [a[0].sum("k"), a[0].contract(a[1], "k")])
+    s, d = oracle_run(prog, [x, y])
+    acc = np.zeros(64, np.float32)
+    for j in range(96):                       # serial f32 fold, left to right
+        acc = (acc + fx[:, j]).astype(np.float32)
+    assert np.array_equal(s, _bf16_trunc(acc))
+    dacc = np.zeros((64, 32), np.float32)
+    for j in range(96):                       # serial k, multiply and add rounded separately
+        dacc = (dacc + (fx[:, j:j + 1] * fy[j:j + 1, :]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(d, _bf16_trunc(dacc))
+    assert (d != _bf16_rne(dacc)).mean() > 0.2
+
+
+def test_tan_and_pow_against_f64():
+    """The oracle's tan and pow (libm tanf / powf, as runCpu binds std.math functions) are within
+    2 ulp of the float64 value, including pow's special cases (x^0 = 1, 1^y = 1, negative bases with
+    integral exponents, NaN for a negative base with a fractional exponent, 0^-1 = inf)."""
+    rng = np.random.default_rng(15)
+    x = np.concatenate([rng.uniform(-1.5, 1.5, 2000), rng.uniform(-100, 100, 2000)]).astype(np.float32)
+    got = oracle_run(T.define("t", [T.spec("f32", i=len(x))], lambda b, a: a[0].tan()), [x])[0].astype(np.float64)
+    ref = np.tan(x.astype(np.float64))
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - ref) <= 2 * ulp).all()
+    base = np.concatenate([rng.uniform(0.05, 20, 3000), [2.0, 1.0, -2.0, -2.0, 0.0, -8.0, 3.0]]).astype(np.float32)
+    expo = np.concatenate([rng.uniform(-8, 8, 3000), [0.0, 123.4, 3.0, 0.5, -1.0, 2.0, 0.0]]).astype(np.float32)
+    got = oracle_run(T.define("p", [T.spec("f32", i=len(base))] * 2, lambda b, a: a[0].pow(a[1])),
+                     [base, expo])[0].astype(np.float64)
+    with np.errstate(all="ignore"):
+        ref = np.power(base.astype(np.float64), expo.astype(np.float64))
+    fin = np.isfinite(ref) & (np.abs(ref) < 3e38) & (np.abs(ref) > 1e-37)
+    ulp = np.spacing(np.abs(ref[fin]).astype(np.float32)).astype(np.float64)
+    assert (np.abs(got[fin] - ref[fin]) <= 2 * ulp).all()
+    assert got[-7] == 1.0 and got[-6] == 1.0 and got[-5] == -8.0
+    assert np.isnan(got[-4]) and got[-3] == np.inf and got[-2] == 64.0 and got[-1] == 1.0
+
+
+@pytest.mark.parametrize("dtype,top", [("u8", 2 ** 8 - 1), ("u16", 2 ** 16 - 1), ("u32", 2 ** 32 - 1),
+                                       ("u64", 2 ** 64 - 1)])
+def test_unsigned_division_by_the_all_ones_value(dtype, top):
+    """Unsigned division is plain truncating division: x / max is 0 below max and 1 at max (an
+    implementation that treats the all-ones divisor as -1 returns 0 - x)."""
+    npd = {"u8": np.uint8, "u16": np.uint16, "u32": np.uint32, "u64": np.uint64}[dtype]
+    x = np.array([5, 0, top, top - 1, 1, top // 2], npd)
+    y = np.array([top] * 6, npd)
+    got = oracle_run(T.define("d", [T.spec(dtype, i=6)] * 2, lambda b, a: a[0].div(a[1])), [x, y])[0]
+    assert list(got) == [0, 0, 1, 0, 0, 0]
 
 
 def test_unary_f32_ops_against_f64():

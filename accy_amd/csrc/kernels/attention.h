@@ -27,7 +27,8 @@
 // operand in distinct LDS arrays so that the compiler's wait analysis can tell the in-flight loads
 // from the reads. Layouts (256-byte rows of 128 elements, conflict-free reads):
 //  * K: 16-byte chunk c of key row r at chunk c ^ (r & 15); A-operand reads are ds_read_b128.
-//  * V: 32-byte unit u of key row r at unit u ^ (r & 7); A-operand reads are ds_read_b64_tr_b16.
+//  * V: 32-byte unit u of key row r at unit u ^ gemm::tr_swizzle(r); A-operand reads are
+//    ds_read_b64_tr_b16 (each 32-lane half covers 256 distinct bytes, the 64-bank LDS's width).
 //
 // The configuration struct C supplies: DT (0 bf16, 1 f16), WAVES, SQ, SK, NB (batch count), the
 // element strides Q_S, K_S, V_S of one query / key row (the head dimension has stride 1), the batch
@@ -80,7 +81,7 @@ __device__ __forceinline__ void load_v(const u16_t* __restrict__ vb, long k0, u1
     const int gi = wave * PER + i;
     const int row = 4 * gi + (lane >> 4);
     const int p = lane & 15;
-    const int u = (p >> 1) ^ (row & 7);
+    const int u = (p >> 1) ^ gemm::tr_swizzle(row);
     gemm::dma16(vb + (k0 + row) * VS + 16 * u + 8 * (p & 1), (ACCY_LDS void*)(lds + gi * 512));
   }
 }
@@ -100,7 +101,7 @@ __device__ __forceinline__ u32x4 v_frag(const u16_t* lds, int dt, int s, int lan
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int k = 16 * s + 8 * r + 4 * (g >> 1) + (i >> 2);
-    const int unit = (n0 >> 4) ^ (k & 7);
+    const int unit = (n0 >> 4) ^ gemm::tr_swizzle(k);
     const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ACCY_LDS i16x4*)(lds + k * HD + unit * 16 + 4 * (i & 3)));
     out[2 * r] = (u32_t)(u16_t)v[0] | ((u32_t)(u16_t)v[1] << 16);
     out[2 * r + 1] = (u32_t)(u16_t)v[2] | ((u32_t)(u16_t)v[3] << 16);

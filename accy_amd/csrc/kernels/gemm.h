@@ -235,11 +235,18 @@ __device__ __forceinline__ void mma16(const u16_t* __restrict__ A, const u16_t* 
 // are in flight under the MFMAs. Each wave waits only for its own loads of the step it consumes
 // (s_waitcnt vmcnt), then one s_barrier (no memory fence) publishes every wave's part.
 //
-// LDS layouts (both conflict-free for the fragment reads of 8 / 16 consecutive lanes):
-//  * K-contiguous operand (rows = M or N, 64 bytes of K per row): 128-byte lines of two rows; the
-//    16-byte chunk at slot s of line L holds logical slot s ^ (L & 7). Fragments: ds_read_b128.
+// LDS layouts. The gfx950 LDS has 64 banks of 4 bytes: a ds_read_b128 is served 16 lanes (256 bytes)
+// per clock and a 64-bit read 32 lanes per clock, so a read is conflict-free when each such lane group
+// covers 256 distinct bytes modulo 256 (measured with SQ_LDS_BANK_CONFLICT: groups that only cover 128
+// distinct bytes take twice the cycles).
+//  * K-contiguous operand (rows = M or N, 64 bytes of K per row): 256-byte lines of four rows; the
+//    16-byte chunk at position p of line L holds logical slot p ^ (L & 3) (slot = 4 (row & 3) + chunk).
+//    A fragment's 16-lane group reads one chunk of 16 consecutive rows: 4 lines x 4 rows, 16 distinct
+//    positions. Fragments: ds_read_b128.
 //  * M/N-contiguous operand (rows = K, BN x 2 bytes per row): the 32-byte unit at position p of row k
-//    holds logical unit p ^ (k & 7). Fragments: ds_read_b64_tr_b16, which hands lane i of each
+//    holds logical unit p ^ tr_swizzle(k), tr_swizzle(k) = 2 (k & 3). A fragment's 32-lane half reads
+//    two adjacent units (u, u ^ 1) of four consecutive rows: eight distinct units modulo 256 bytes.
+//    Fragments: ds_read_b64_tr_b16, which hands lane i of each
 //    16-lane group element (i mod 4) of the 8 bytes addressed by lane 4t + i / 4 as its element t;
 //    pointing lane j of the group at row k0 + j / 4, columns n0 + 4 (j mod 4) .. + 3 gives lane i the
 //    4 values B[k0 .. k0 + 3][n0 + i], the MFMA B-operand layout (and likewise for A).
@@ -249,6 +256,9 @@ __device__ __forceinline__ void mma16(const u16_t* __restrict__ A, const u16_t* 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void dma16(const void* g, ACCY_LDS void* l) { __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0); }
+
+// Unit swizzle of an M/N-contiguous (transposed-read) tile row k: see the layouts above.
+__device__ __forceinline__ int tr_swizzle(int k) { return 2 * (k & 3); }
 
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -305,8 +315,9 @@ __device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0
   const int gi = wave * (INSTRS / 4) + i;
   const u16_t* src;
   if constexpr (KC) {
-    const int q = (lane & 7) ^ (lane >> 3);  // logical slot of this lane's physical chunk
-    const int row = 16 * gi + 2 * (lane >> 3) + (q >> 2);
+    // instruction gi fills lines 4 gi .. 4 gi + 3: lane l writes position l & 15 of line 4 gi + l / 16
+    const int q = (lane & 15) ^ (lane >> 4);  // logical slot of this lane's physical chunk
+    const int row = 16 * gi + 4 * (lane >> 4) + (q >> 2);
     long r = r0 + row;
     if constexpr (RAGGED) r = r < RMAX ? r : RMAX - 1;
     src = base + O::row(r) + O::k(k0) + 8 * (q & 3);
@@ -317,7 +328,7 @@ __device__ __forceinline__ void dma_part(const u16_t* __restrict__ base, long r0
     constexpr int RPI = 1024 / ROWB;  // k rows per instruction
     const int row = RPI * gi + lane / LPR;
     const int p = lane % LPR;
-    const int u = (p >> 1) ^ (row & 7);
+    const int u = (p >> 1) ^ tr_swizzle(row);
     if constexpr (RAGGED) {
       long col = r0 + 16 * u + 8 * (p & 1);
       col = col <= RMAX - 8 ? col : RMAX - 8;
@@ -341,8 +352,8 @@ template <int ROWS, bool KC>
 __device__ __forceinline__ u32x4 frag(const u16_t* lds, int row0, int s, int lane) {
   if constexpr (KC) {
     const int r = row0 + (lane & 31), c = 2 * s + (lane >> 5);
-    const int line = r >> 1, slot = ((r & 1) << 2) | c;
-    return *(const u32x4*)(lds + line * 64 + ((slot ^ (line & 7)) << 3));
+    const int line = r >> 2, slot = ((r & 3) << 2) | c;
+    return *(const u32x4*)(lds + line * 128 + ((slot ^ (line & 3)) << 3));
   } else {
     constexpr int ROWE = ROWS;  // elements per k row
     const int g = lane >> 4, i = lane & 15;
@@ -351,7 +362,7 @@ __device__ __forceinline__ u32x4 frag(const u16_t* lds, int row0, int s, int lan
 #pragma unroll
     for (int rr = 0; rr < 2; ++rr) {
       const int k = 16 * s + 8 * (g >> 1) + 4 * rr + (i >> 2);
-      const int unit = (n0 >> 4) ^ (k & 7);
+      const int unit = (n0 >> 4) ^ tr_swizzle(k);
       const u16_t* p = lds + k * ROWE + unit * 16 + 4 * (i & 3);
       const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ACCY_LDS i16x4*)p);
       const u32_t lo = (u32_t)(u16_t)v[0] | ((u32_t)(u16_t)v[1] << 16);

@@ -11,6 +11,7 @@
 
 #include "plan.hpp"
 #include "runtime.hpp"
+#include "scratch.hpp"
 #include "tuning.hpp"
 #include "wire.hpp"
 
@@ -229,6 +230,26 @@ int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t 
     if (n_inputs && !inputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
     if (n_outputs && !outputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
     ex->invoke_device(inputs, n_inputs, outputs, n_outputs, (hipStream_t)stream);
+    return ACCY_HIP_OK;
+  });
+}
+
+int accy_hip_invoke_device_scratch(accy_hip_handle h, const void* const* inputs, size_t n_inputs,
+                                   void* const* outputs, size_t n_outputs, void* stream) {
+  std::shared_ptr<Executor> ex = hold(h);
+  if (!ex) return fail_with(ACCY_HIP_INVALID_HANDLE, "stale or unknown handle");
+  return guarded([&]() -> int {
+    if (n_inputs && !inputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null input list");
+    if (n_outputs && !outputs) return fail_with(ACCY_HIP_INVALID_BUFFER, "null output list");
+    if (ex->scratch_bytes() > kScratchBytes)
+      return fail_with(ACCY_HIP_OUT_OF_MEMORY, "the program's intermediate buffers need " +
+                                                   std::to_string(ex->scratch_bytes()) +
+                                                   " bytes; the device scratch holds " +
+                                                   std::to_string(kScratchBytes));
+    void* base = nullptr;
+    const char* why = "";
+    if (scratch_region(&base, &why) != 0) return fail_with(ACCY_HIP_LAUNCH_FAILED, std::string("device scratch: ") + why);
+    ex->invoke_device(inputs, n_inputs, outputs, n_outputs, (hipStream_t)stream, (uint8_t*)base);
     return ACCY_HIP_OK;
   });
 }

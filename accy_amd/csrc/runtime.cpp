@@ -147,6 +147,24 @@ Executor::Executor(Program program, Plan plan) : program_(std::move(program)), p
         check(hipMalloc(&loop_bufs_[i][nc + c], bytes), "hipMalloc");
       }
     }
+    // Scratch layout for allocation-free invocations: each intermediate buffer gets its own 256-byte
+    // aligned range (temporaries, then per loop its carry buffers and its body's scratch).
+    auto take = [&](uint64_t bytes) {
+      const uint64_t off = scratch_total_;
+      scratch_total_ += (bytes + 255) & ~uint64_t(255);
+      return off;
+    };
+    scratch_off_.assign(plan_.slots.size(), 0);
+    for (size_t i = 0; i < plan_.slots.size(); ++i)
+      if (plan_.slots[i].role == SlotInfo::Temp) scratch_off_[i] = take(plan_.slots[i].bytes);
+    loop_scratch_off_.resize(plan_.steps.size());
+    for (size_t i = 0; i < plan_.steps.size(); ++i) {
+      if (plan_.steps[i].type != Step::Loop) continue;
+      const Plan& bp = *plan_.steps[i].loop.plan;
+      const size_t nc = bp.input_slots.size();
+      for (size_t b = 0; b < 2 * nc; ++b) loop_scratch_off_[i].push_back(take(bp.slots[(size_t)bp.input_slots[b % nc]].bytes));
+      loop_scratch_off_[i].push_back(take(loops_[i]->scratch_bytes()));
+    }
     int dev = 0, max_lds = 0;
     check(hipGetDevice(&dev), "hipGetDevice");
     check(hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "hipDeviceGetAttribute");
@@ -188,11 +206,17 @@ Executor::~Executor() {
 
 // Carries start as copies of the initial values; each iteration runs the body from one buffer set
 // into the other on the same stream; the final carries are copied to the slots that read them.
-void Executor::run_loop(size_t step, hipStream_t stream) {
+void Executor::run_loop(size_t step, hipStream_t stream, uint8_t* scratch) {
   const LoopStep& L = plan_.steps[step].loop;
   const Plan& bp = *L.plan;
   const size_t nc = bp.input_slots.size();
-  std::vector<void*>& buf = loop_bufs_[step];
+  std::vector<void*> from_scratch;
+  if (scratch) {
+    from_scratch.resize(2 * nc);
+    for (size_t b = 0; b < 2 * nc; ++b) from_scratch[b] = scratch + loop_scratch_off_[step][b];
+  }
+  std::vector<void*>& buf = scratch ? from_scratch : loop_bufs_[step];
+  uint8_t* body_scratch = scratch ? scratch + loop_scratch_off_[step][2 * nc] : nullptr;
   auto bytes = [&](size_t c) { return bp.slots[(size_t)bp.input_slots[c]].bytes; };
   for (size_t c = 0; c < nc; ++c)
     if (bytes(c))
@@ -206,7 +230,7 @@ void Executor::run_loop(size_t step, hipStream_t stream) {
       in[c] = buf[cur * nc + c];
       out[c] = buf[(1 - cur) * nc + c];
     }
-    loops_[step]->invoke_device(in.data(), nc, out.data(), nc, stream);
+    loops_[step]->invoke_device(in.data(), nc, out.data(), nc, stream, body_scratch);
     cur = 1 - cur;
   }
   for (size_t c = 0; c < nc; ++c)
@@ -245,13 +269,15 @@ const std::vector<KernelTiming>& Executor::timings() {
   return timings_;
 }
 
-void Executor::run_steps(hipStream_t stream) {
-  for (size_t i = 0; i < plan_.slots.size(); ++i)
-    if (plan_.slots[i].role == SlotInfo::Temp || plan_.slots[i].role == SlotInfo::Const) bound_[i] = owned_[i];
-  // Event slot of this invocation when profiling (created on first use).
+void Executor::run_steps(hipStream_t stream, uint8_t* scratch) {
+  for (size_t i = 0; i < plan_.slots.size(); ++i) {
+    if (plan_.slots[i].role == SlotInfo::Const) bound_[i] = owned_[i];
+    if (plan_.slots[i].role == SlotInfo::Temp) bound_[i] = scratch ? scratch + scratch_off_[i] : owned_[i];
+  }
+  // Event slot of this invocation when profiling (created on first use; never with scratch).
   const size_t nk = timings_.size();
   hipEvent_t* ev = nullptr;
-  if (profiling_ && nk) {
+  if (profiling_ && nk && !scratch) {
     const size_t slot = recorded_ % kProfiledCalls;
     if (events_.size() < (slot + 1) * nk * 2) {
       size_t old = events_.size();
@@ -270,7 +296,7 @@ void Executor::run_steps(hipStream_t stream) {
       continue;
     }
     if (st.type == Step::Loop) {
-      run_loop(i, stream);
+      run_loop(i, stream, scratch);
       continue;
     }
     const KernelStep& k = st.kernel;
@@ -294,7 +320,7 @@ void Executor::run_steps(hipStream_t stream) {
 }
 
 void Executor::invoke_device(const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs,
-                             hipStream_t stream) {
+                             hipStream_t stream, uint8_t* scratch) {
   if (n_inputs != plan_.input_slots.size() || n_outputs != plan_.output_slots.size())
     throw HipFailure(kStatusInvalidBuffer, "buffer count mismatch");
   // Buffers are used in place and the kernels read and write them with 16-byte vector accesses
@@ -318,7 +344,7 @@ void Executor::invoke_device(const void* const* inputs, size_t n_inputs, void* c
   }
   for (size_t i = 0; i < n_inputs; ++i) bound_[(size_t)plan_.input_slots[i]] = const_cast<void*>(inputs[i]);
   for (size_t i = 0; i < n_outputs; ++i) bound_[(size_t)plan_.output_slots[i]] = outputs[i];
-  run_steps(stream);
+  run_steps(stream, scratch);
 }
 
 void Executor::invoke_host(const void* const* inputs, const size_t* input_lens, size_t n_inputs,

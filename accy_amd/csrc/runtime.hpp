@@ -63,9 +63,15 @@ class Executor {
   // Host slices in, host slices out; sizes must equal the descriptors' byte sizes.
   void invoke_host(const void* const* inputs, const size_t* input_lens, size_t n_inputs, void* const* outputs,
                    const size_t* output_lens, size_t n_outputs);
-  // Device pointers in and out, enqueued on `stream`, no synchronisation.
+  // Device pointers in and out, enqueued on `stream`, no synchronisation. With `scratch` set, every
+  // intermediate buffer of the run (temporaries, scan carries, the scan bodies' temporaries) is taken
+  // from [scratch, scratch + scratch_bytes()) instead of the executor's own allocations, and no
+  // profiling events are recorded: the call then allocates no device memory and creates no object.
   void invoke_device(const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs,
-                     hipStream_t stream);
+                     hipStream_t stream, uint8_t* scratch = nullptr);
+  // Bytes of device scratch an invocation with `scratch` uses: every intermediate buffer at its own
+  // 256-byte aligned offset (no reuse between buffers).
+  uint64_t scratch_bytes() const { return scratch_total_; }
 
   // While profiling is on, every invocation records a HIP event pair around each kernel on the
   // launch stream (no synchronisation, so back-to-back invocations keep their steady state);
@@ -76,7 +82,7 @@ class Executor {
   const std::vector<KernelTiming>& timings();
 
  private:
-  void run_steps(hipStream_t stream);
+  void run_steps(hipStream_t stream, uint8_t* scratch);
   Program program_;
   Plan plan_;
   std::vector<void*> owned_;     // device allocation per slot (Temp / Const; staging for Input / Output)
@@ -91,7 +97,12 @@ class Executor {
   // Loop steps: the body's executor and two sets of carry buffers (carries in / out), per step.
   std::vector<std::unique_ptr<Executor>> loops_;
   std::vector<std::vector<void*>> loop_bufs_;
-  void run_loop(size_t step, hipStream_t stream);
+  void run_loop(size_t step, hipStream_t stream, uint8_t* scratch);
+  // Scratch layout: offset of each temporary slot, and per loop step the offsets of its 2 x carries
+  // buffers followed by the offset of its body's own scratch.
+  std::vector<uint64_t> scratch_off_;
+  std::vector<std::vector<uint64_t>> loop_scratch_off_;
+  uint64_t scratch_total_ = 0;
 };
 
 int device_count();

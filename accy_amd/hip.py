@@ -89,7 +89,7 @@ _lib = None
 _lib_lock = threading.Lock()
 
 EXPORTS = ["accy_hip_run", "accy_hip_compile", "accy_hip_counts", "accy_hip_describe", "accy_hip_invoke",
-           "accy_hip_invoke_device", "accy_hip_release", "accy_hip_last_error", "accy_hip_set_profiling",
+           "accy_hip_invoke_device", "accy_hip_invoke_device_scratch", "accy_hip_release", "accy_hip_last_error", "accy_hip_set_profiling",
            "accy_hip_kernel_count", "accy_hip_kernel_info", "accy_hip_plan_source", "accy_hip_device_arch",
            "accy_hip_malloc", "accy_hip_free", "accy_hip_memcpy", "accy_hip_stream_create",
            "accy_hip_stream_destroy", "accy_hip_stream_synchronize", "accy_hip_event_create",
@@ -114,6 +114,7 @@ def library() -> ctypes.CDLL:
         lib.accy_hip_describe.argtypes = [Handle, ctypes.c_int, sz, ctypes.POINTER(_Descriptor)]
         lib.accy_hip_invoke.argtypes = [Handle, vpp, szp, sz, vpp, szp, sz]
         lib.accy_hip_invoke_device.argtypes = [Handle, vpp, sz, vpp, sz, vp]
+        lib.accy_hip_invoke_device_scratch.argtypes = [Handle, vpp, sz, vpp, sz, vp]
         lib.accy_hip_release.argtypes = [Handle]
         lib.accy_hip_last_error.restype = ctypes.c_char_p
         lib.accy_hip_set_profiling.argtypes = [Handle, ctypes.c_int]

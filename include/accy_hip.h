@@ -105,6 +105,18 @@ int accy_hip_invoke(accy_hip_handle h, const void* const* inputs, const size_t* 
 int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t n_inputs, void* const* outputs,
                            size_t n_outputs, void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): accy_hip_invoke_device with
+ * every intermediate buffer of the run (temporaries between kernels, chunked-fold partials, scan
+ * carries) placed in one static device array of 512 MiB that each GPU the library runs on holds until
+ * the process ends, instead of the program's own allocations. It calls no hipMalloc / hipFree and
+ * records no profiling events. A program whose intermediates need more than 512 MiB returns
+ * ACCY_HIP_OUT_OF_MEMORY before anything is launched. Every call on one GPU uses the same array and
+ * leaves the last call's contents in it (each kernel writes an intermediate in full before it is
+ * read, so nothing needs clearing): calls that overlap on one GPU, on any streams, race. */
+int accy_hip_invoke_device_scratch(accy_hip_handle h, const void* const* inputs, size_t n_inputs,
+                                   void* const* outputs, size_t n_outputs, void* stream);
+
 /* `Cpu.deinit` / `Session.release` (session.zig:216-226). */
 int accy_hip_release(accy_hip_handle h);
 

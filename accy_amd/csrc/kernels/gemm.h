@@ -53,18 +53,29 @@ __device__ __forceinline__ void transpose8x8(const u32x4 (&in)[8], u32x4 (&out)[
   }
 }
 
-// Tile numbering: dispatch order round-robins workgroups over the 8 XCDs; give each XCD a
-// contiguous range of tiles, then walk that range in groups of GROUP_M tile rows.
+// Dispatch order round-robins workgroups over the 8 XCDs: the index of workgroup `bid` when each
+// XCD instead takes a contiguous range of the TOTAL indices.
+template <long TOTAL>
+__device__ __forceinline__ long xcd_contiguous(long bid) {
+  if constexpr (TOTAL % 8 == 0) bid = (bid % 8) * (TOTAL / 8) + bid / 8;
+  return bid;
+}
+
+// Tile of index `bid` when the tiles are walked in groups of GROUP_M tile rows.
 template <long TILES_M, long TILES_N, int GROUP_M>
-__device__ __forceinline__ void tile_of(long bid, long& tm, long& tn) {
-  constexpr long TILES = TILES_M * TILES_N;
-  if constexpr (TILES % 8 == 0) bid = (bid % 8) * (TILES / 8) + bid / 8;
+__device__ __forceinline__ void tile_in_groups(long bid, long& tm, long& tn) {
   const long per_group = (long)GROUP_M * TILES_N;
   const long group = bid / per_group;
   const long first_m = group * GROUP_M;
   const long gsize = (TILES_M - first_m) < GROUP_M ? (TILES_M - first_m) : GROUP_M;
   tm = first_m + (bid % per_group) % gsize;
   tn = (bid % per_group) / gsize;
+}
+
+// Tile numbering: each XCD works on a contiguous range of tiles, walked in groups of GROUP_M rows.
+template <long TILES_M, long TILES_N, int GROUP_M>
+__device__ __forceinline__ void tile_of(long bid, long& tm, long& tn) {
+  tile_in_groups<TILES_M, TILES_N, GROUP_M>(xcd_contiguous<TILES_M * TILES_N>(bid), tm, tn);
 }
 
 // Loads one operand tile (ROWS rows of the operand's M or N, BK values of K) into registers.
@@ -488,7 +499,8 @@ struct DmaGroup {
 // 128 KiB, one workgroup per CU; 3 with 256 x 128: 72 KiB, two per CU when the kernel is compiled for
 // two waves per SIMD, so that one workgroup's epilogue runs beside the other's matrix work).
 template <class C, class Epi>
-__device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi) {
+__device__ __forceinline__ void mma16_dma_tile(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi,
+                                               long tm, long tn) {
   constexpr int BM = C::BM, BN = C::BN, S = C::STAGES;
   constexpr int TM = BM / 64, TN = BN / 64;
   constexpr long TILES_M = (C::M + BM - 1) / BM, TILES_N = (C::N + BN - 1) / BN, KT = C::K / 32;
@@ -512,8 +524,8 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  long tm, tn;
-  tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
+  (void)TILES_M;
+  (void)TILES_N;
   const long m0 = tm * BM, n0 = tn * BN, batch = blockIdx.y;
   const u16_t* __restrict__ Ab = A + C::a_b(batch);
   const u16_t* __restrict__ Bb = B + C::b_b(batch);
@@ -558,6 +570,32 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
         }
 }
 
+template <class C, class Epi>
+__device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi) {
+  constexpr long TILES_M = (C::M + C::BM - 1) / C::BM, TILES_N = (C::N + C::BN - 1) / C::BN;
+  long tm, tn;
+  tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
+  mma16_dma_tile<C>(A, B, epi, tm, tn);
+}
+
+// G contractions that share the A operand, every extent and both layouts, each with its own B
+// operand and output, in one launch of G x tiles workgroups (the projections of one activation:
+// one fill and drain of the machine instead of G). Consecutive indices of an XCD's range take the G
+// contractions of one tile, so the workgroups that read an A row panel run on the same XCD (its L2)
+// at about the same time. The epilogue functor takes the contraction index first: epi(g, b, m, n, v).
+template <class C, int G, class Epi>
+__device__ __forceinline__ void mma16_dma_group(const u16_t* __restrict__ A, const u16_t* const (&B)[G], const Epi& epi) {
+  constexpr long TILES_M = (C::M + C::BM - 1) / C::BM, TILES_N = (C::N + C::BN - 1) / C::BN;
+  const long bid = xcd_contiguous<G * TILES_M * TILES_N>((long)blockIdx.x);
+  const int g = (int)(bid % G);
+  long tm, tn;
+  tile_in_groups<TILES_M, TILES_N, 8>(bid / G, tm, tn);
+  const u16_t* __restrict__ Bg = B[0];
+#pragma unroll
+  for (int i = 1; i < G; ++i)
+    if (g == i) Bg = B[i];
+  mma16_dma_tile<C>(A, Bg, [&](long b, long m, long n, float v) { epi(g, b, m, n, v); }, tm, tn);
+}
 
 // ---------------------------------------------------------------------------------------------
 // f32 contraction on v_mfma_f32_32x32x2_f32 (exact f32 products, f32 accumulation).

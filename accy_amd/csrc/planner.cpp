@@ -1697,10 +1697,125 @@ class Planner {
     GemmShape gs;
     if (gemm_eligible(op, gs)) {
       if (op.result.dtype == DType::f32 && !f32_layout_ok(gs)) pack_f32_operands(gs);
+      std::vector<std::pair<uint32_t, GemmShape>> group;
+      if (gemm_siblings(v, gs, group)) {
+        gemm_group(group);
+        return;
+      }
       gemm(v, gs);
       return;
     }
     dot_serial(v);
+  }
+
+  // ---- grouped contractions: several contractions of one activation in one launch ----
+  //
+  // dot_general v and the later, not yet planned contractions u with the same A view (same buffer,
+  // offset and layout), the same extents and the same B layout, whose B operands are already
+  // available and whose results are plain stores (no fused epilogue, no attention): the projections
+  // of one normalised activation. They run as one direct-to-LDS launch of G x tiles workgroups
+  // (mma16_dma_group), so the machine fills and drains once instead of G times. Every output keeps
+  // its own k order and accumulation, so the results are those of separate launches bit for bit.
+  static bool same_group(const Group& x, const Group& y) { return x.ext == y.ext && x.str == y.str; }
+
+  bool plain_store(uint32_t u) const {
+    uint32_t t;
+    return attn_.find(u) == attn_.end() && !epilogue_target(u, t);
+  }
+
+  bool gemm_siblings(uint32_t v, const GemmShape& gs, std::vector<std::pair<uint32_t, GemmShape>>& group) const {
+    const Op& op = g_.ops[v];
+    const DType d = op.result.dtype;
+    if (op.kind != Kind::dot_general || (d != DType::bf16 && d != DType::f16) || gs.multi) return false;
+    if (gs.m % 256 != 0 || gs.n % 256 != 0 || std::getenv("ACCY_GEMM_NO_GROUP")) return false;
+    int dm = 0, dn = 0;
+    bool akc = gs.a_k == 1, bkc = gs.b_k == 1;
+    if (!dma_eligible(gs, dm, dn, akc, bkc) || dm != 256 || dn != 256 || !plain_store(v)) return false;
+    group.assign(1, {v, gs});
+    constexpr size_t kMaxGroup = 4;
+    for (uint32_t u = v + 1; u < g_.ops.size() && group.size() < kMaxGroup; ++u) {
+      const Op& uo = g_.ops[u];
+      if (!live_[u] || done_[u] || uo.kind != Kind::dot_general || uo.args[0] != op.args[0] || uo.result.dtype != d)
+        continue;
+      GemmShape gu;
+      if (!gemm_eligible(uo, gu) || gu.multi || !plain_store(u)) continue;
+      if (gu.batch != gs.batch || gu.m != gs.m || gu.n != gs.n || gu.k != gs.k) continue;
+      if (gu.a.slot != gs.a.slot || gu.a.offset != gs.a.offset || gu.a_b != gs.a_b || gu.a_m != gs.a_m ||
+          gu.a_k != gs.a_k || gu.b_b != gs.b_b || gu.b_k != gs.b_k || gu.b_n != gs.b_n)
+        continue;
+      if (!same_group(gu.ga_b, gs.ga_b) || !same_group(gu.ga_m, gs.ga_m) || !same_group(gu.ga_k, gs.ga_k) ||
+          !same_group(gu.gb_b, gs.gb_b) || !same_group(gu.gb_k, gs.gb_k) || !same_group(gu.gb_n, gs.gb_n))
+        continue;
+      int um = 0, un = 0;
+      bool uak = gu.a_k == 1, ubk = gu.b_k == 1;
+      if (!dma_eligible(gu, um, un, uak, ubk) || um != dm || un != dn || uak != akc || ubk != bkc) continue;
+      group.push_back({u, gu});
+    }
+    return group.size() > 1;
+  }
+
+  void gemm_group(const std::vector<std::pair<uint32_t, GemmShape>>& group) {
+    const uint32_t v = group[0].first;
+    const GemmShape& gs = group[0].second;
+    const DType d = g_.ops[v].result.dtype;
+    const size_t G = group.size();
+    KernelWriter w(g_, slots_, "i64_t");
+    const std::string a = w.arg(gs.a.slot, false);
+    std::vector<std::string> bs;
+    std::ostringstream cases;
+    const std::string cidx = "b * " + std::to_string(gs.m * gs.n) + "L + m * " + std::to_string(gs.n) + "L + n";
+    std::string nm = name("gemm", v), label = "gemm:%" + std::to_string(v);
+    for (size_t i = 0; i < G; ++i) {
+      const uint32_t u = group[i].first;
+      bs.push_back(w.arg(group[i].second.b.slot, false) + " + " + std::to_string(group[i].second.b.offset) + "L");
+      const int out = slots_.slot_of[u] >= 0 ? slots_.slot_of[u] : temp_slot(u);
+      cases << "      case " << i << ": " << w.store(out, cidx, d, "v") << " break;\n";
+      if (i) label += "&%" + std::to_string(u);
+    }
+    std::ostringstream members, inits;
+    {
+      std::string pl = w.params();
+      size_t start = 0;
+      while (start < pl.size()) {
+        size_t comma = pl.find(", ", start);
+        std::string decl = pl.substr(start, comma == std::string::npos ? std::string::npos : comma - start);
+        members << "  " << decl << ";\n";
+        size_t sp = decl.rfind(' ');
+        inits << (inits.tellp() > 0 ? ", " : "") << decl.substr(sp + 1);
+        if (comma == std::string::npos) break;
+        start = comma + 2;
+      }
+    }
+    std::ostringstream src;
+    src << "#include \"gemm\"\n";
+    src << "struct Epi_" << nm << " {\n" << members.str()
+        << "  __device__ __forceinline__ void operator()(int g, long b, long m, long n, float v) const {\n"
+        << "    switch (g) {\n" << cases.str() << "    }\n  }\n};\n";
+    src << "struct Cfg_" << nm << " {\n"
+        << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
+        << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"
+        << "  static constexpr long A_B = " << gs.a_b << ", A_M = " << gs.a_m << ", A_K = " << gs.a_k << ";\n"
+        << "  static constexpr long B_B = " << gs.b_b << ", B_K = " << gs.b_k << ", B_N = " << gs.b_n << ";\n"
+        << "  static constexpr bool A_KC = " << (gs.a_k == 1 ? "true" : "false")
+        << ", B_KC = " << (gs.b_k == 1 ? "true" : "false") << ";\n"
+        << gs.ga_b.fn("a_b") << gs.ga_m.fn("a_m") << gs.ga_k.fn("a_k") << gs.gb_b.fn("b_b") << gs.gb_k.fn("b_k")
+        << gs.gb_n.fn("b_n") << "  static constexpr int BM = 256, BN = 256, STAGES = 4;\n};\n";
+    src << "extern \"C\" __global__ void __launch_bounds__(256) " << nm << "(" << w.params() << ") {\n"
+        << "  const u16_t* const bs[" << G << "] = {";
+    for (size_t i = 0; i < G; ++i) src << (i ? ", " : "") << bs[i];
+    src << "};\n  accy::gemm::mma16_dma_group<Cfg_" << nm << ", " << G << ">(" << a << " + " << gs.a.offset
+        << "L, bs, Epi_" << nm << "{" << inits.str() << "});\n}\n";
+    KernelStep k;
+    k.source = src.str();
+    k.name = nm;
+    k.grid[0] = (uint32_t)(G * (size_t)((gs.m / 256) * (gs.n / 256)));
+    k.grid[1] = (uint32_t)gs.batch;
+    k.block[0] = 256;
+    k.klass = "gemm";
+    k.label = label;
+    k.algorithmic_flops = 2.0 * (double)G * (double)gs.batch * (double)gs.m * (double)gs.n * (double)gs.k;
+    push(std::move(k), w);
+    for (const auto& member : group) finish(member.first);
   }
 
   // Output layout of a contraction result: strides of the flattened batch, m and n groups.

@@ -28,6 +28,7 @@ import ctypes
 import json
 import math
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -52,12 +53,13 @@ TRAFFIC = Path(__file__).resolve().parent / "profiles" / "traffic.json"
 
 def measured_traffic(config: str, label: str):
     """HBM bytes per launch of one kernel from the committed rocprofv3 counter measurement
-    (FETCH_SIZE and WRITE_SIZE, calibrated on a copy kernel), or None when not measured."""
+    (FETCH_SIZE and WRITE_SIZE, calibrated on a copy kernel), or None when not measured. A label with
+    a fused epilogue (+) or a grouped launch (&) is keyed by its first value."""
     try:
         table = json.loads(TRAFFIC.read_text()).get(config, {})
     except (OSError, ValueError):
         return None
-    return table.get(label, table.get(label.split("+")[0]))
+    return table.get(label, table.get(re.split("[+&]", label)[0]))
 
 
 VALU = Path(__file__).resolve().parent / "profiles" / "valu.json"
@@ -74,7 +76,7 @@ def measured_valu(config: str, label: str):
         table = json.loads(VALU.read_text()).get(config, {})
     except (OSError, ValueError):
         return None
-    return table.get(label, table.get(label.split("+")[0]))
+    return table.get(label, table.get(re.split("[+&]", label)[0]))
 
 
 def decoder_flops(batch, seq, model, heads, hd, ffn):
@@ -178,7 +180,7 @@ def oracle_time(cfg, budget_s: float):
                                  sample=f"median of {n_one} runs, {t_one:.3f} s each"))
 
 
-def measure(name: str, cfg: dict, steps: int, warmup: int) -> dict:
+def measure(name: str, cfg: dict, steps: int, warmup: int, warmup_s: float) -> dict:
     """Runs one config on the GPU: K timed steps over HBM-resident inputs, then K profiled steps for
     the per-kernel durations. Returns the step time, the throughput and the dominant kernel's
     roofline entry."""
@@ -195,9 +197,18 @@ def measure(name: str, cfg: dict, steps: int, warmup: int) -> dict:
     def step():
         ex.launch_device(iptr, optr, stream.handle)
 
-    for _ in range(warmup):
-        step()
+    # Warmup in chunks of about 20 ms of device work, one synchronisation per chunk (a gap between
+    # launches would let the clock recover and the timed steps would not see the sustained state).
+    t_w = time.perf_counter()
+    step()
     stream.synchronize()
+    done = 1
+    chunk = max(1, int(0.02 / max(time.perf_counter() - t_w, 1e-6)))
+    while done < warmup or time.perf_counter() - t_w < warmup_s:
+        for _ in range(chunk):
+            step()
+        done += chunk
+        stream.synchronize()
     start, end = hip.Event(), hip.Event()
     t0 = time.perf_counter()
     start.record(stream)
@@ -245,7 +256,7 @@ def measure(name: str, cfg: dict, steps: int, warmup: int) -> dict:
     for b in dins + douts:
         b.free()
     stream.destroy()
-    return dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"],
+    return dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"], warmup=done,
                 workload=dict(workload=name, **cfg["workload"]), roofline=roof,
                 kernels={lbl: float(k.mean_ms) for lbl, k in per_kernel.items()})
 
@@ -258,10 +269,13 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # Under sustained matrix-core load the power controller first drops the clock (a bf16 8192^3
-    # contraction goes from about 0.82 to 1.08 ms per launch within four launches) and then settles
-    # over the next ~20 launches near 0.80 ms; 30 warmup steps put the timed steps in that steady state.
-    ap.add_argument("--warmup", type=int, default=30)
+    # Under sustained back-to-back launches the power controller first lowers the clock (a bf16 8192^3
+    # contraction goes from about 0.82 to 1.08 ms per launch within four launches, the C2 row kernel
+    # from 0.156 to 0.213 ms within 20) and then settles over some milliseconds. Warmup runs at least
+    # --warmup steps and at least --warmup-seconds of them, so the timed steps measure the sustained
+    # steady state; the line reports the number of warmup steps actually run.
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup-seconds", type=float, default=0.2)
     ap.add_argument("--config", default="all",
                     help="'all' (the headline C2 line plus every config under 'configs') or one config")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
@@ -278,21 +292,22 @@ def main() -> int:
     results = {}
     for name in names:
         print(f"bench: {name}", file=sys.stderr, flush=True)
-        r = measure(name, cfgs[name], args.steps, args.warmup)
+        r = measure(name, cfgs[name], args.steps, args.warmup, args.warmup_seconds)
         budget = args.cpu_budget if name == head else args.cpu_budget / 3
         r["cpu_baseline"] = None if args.no_cpu else oracle_time(cfgs[name], budget)
         results[name] = r
     h = results[head]
     line = {
         "metric": METRIC, "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "warmup": h["warmup"], "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": h["dtype"], "data": "synthetic (seeded SplitMix64)",
         "config": h["workload"], "roofline": h["roofline"], "cpu_baseline": h["cpu_baseline"],
         "kernels": h["kernels"],
     }
     if len(names) > 1:
         line["configs"] = {
-            n: dict(ms=r["ms_per_step"], value=r["value"], unit=r["unit"], dtype=r["dtype"], bound=r["roofline"]["bound"],
+            n: dict(ms=r["ms_per_step"], value=r["value"], unit=r["unit"], dtype=r["dtype"], warmup=r["warmup"],
+                    bound=r["roofline"]["bound"],
                     kernel=r["roofline"]["kernel"], kernel_ms=r["roofline"]["kernel_ms"],
                     achieved=r["roofline"]["achieved"], peak=r["roofline"]["peak"],
                     roofline_unit=r["roofline"]["unit"], frac=r["roofline"]["frac"],

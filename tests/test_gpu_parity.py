@@ -231,6 +231,26 @@ def test_attention_full_size_on_sampled_heads():
     assert_attention(got[heads], ref, 2e-2, "f16", exact_attention(*sub, _scale("f16"), False, "f16"))
 
 
+def test_grouped_projections_equal_separate_launches():
+    """Contractions of one activation with the same extents and layouts (a decoder block's q, k and v
+    projections) run as one grouped launch; each output keeps its own k order, so the results equal
+    separate launches (ACCY_GEMM_NO_GROUP) bit for bit, and match the oracle."""
+    import os
+    prog = W.decoder_program(1, 256, 512, 4, 128, 1024)
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "mma16_dma_group" in src and "&%" in src
+    ins = W.decoder_inputs(1, 256, 512, 4, 128, 1024, seed=12)
+    grouped = hip_run(prog, ins)[0]
+    os.environ["ACCY_GEMM_NO_GROUP"] = "1"
+    try:
+        assert "mma16_dma_group" not in hip.plan_source(prog.encode(), compile=False)
+        separate = hip_run(prog, ins)[0]
+    finally:
+        del os.environ["ACCY_GEMM_NO_GROUP"]
+    assert np.array_equal(grouped, separate)
+    assert_rowwise(grouped, oracle_run(prog, ins)[0], 2e-2, "bf16")
+
+
 def test_decoder_with_fused_causal_attention():
     say("decoder 1 x 128 x 256, 2 heads x 128, ffn 512, bf16")
     prog = W.decoder_program(1, 128, 256, 2, 128, 512, dtype="bf16")

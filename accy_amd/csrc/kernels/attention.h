@@ -1,5 +1,6 @@
 // Fused attention O[b, q, :] = softmax_k(scale * Q[b, q, :] . K[b, k, :] [masked k > q]) V[b, k, :] on
-// gfx950 matrix cores, for 16-bit Q, K, V with a head dimension of 128 (both for Q.K and for V).
+// gfx950 matrix cores, for 16-bit Q, K, V with a head dimension HD of 64 or 128 (both for Q.K and for
+// V), and (flash_f32, at the end) for f32 Q, K, V with a head dimension of 64.
 //
 // A workgroup of 2 * WAVES wavefronts owns 64 * WAVES queries of one batch index and streams the
 // keys in blocks of 32. Each group of 64 queries (two 32-query tiles, q0 + 32 w and
@@ -30,7 +31,7 @@
 //  * V: 32-byte unit u of key row r at unit u ^ gemm::tr_swizzle(r); A-operand reads are
 //    ds_read_b64_tr_b16 (each 32-lane half covers 256 distinct bytes, the 64-bank LDS's width).
 //
-// The configuration struct C supplies: DT (0 bf16, 1 f16), WAVES, SQ, SK, NB (batch count), the
+// The configuration struct C supplies: DT (0 bf16, 1 f16), HD, WAVES, SQ, SK, NB (batch count), the
 // element strides Q_S, K_S, V_S of one query / key row (the head dimension has stride 1), the batch
 // offset functions q_off(b), k_off(b), v_off(b), CAUSAL and SL (the score scale times log2 e, > 0).
 // O is written row-major as [b][q][128]. The kernel is launched with 128 * WAVES threads.
@@ -57,43 +58,55 @@ template <int B, int E> struct For {
   }
 };
 
-constexpr int HD = 128;  // head dimension of Q, K and V
 constexpr int BK = 32;   // keys per block
 
-// Issues this wave's share of the K tile of keys [k0, k0 + 32): 8 instructions of 4 rows each.
-template <int WAVES, long KS>
+// LDS layouts of a K / V tile (32 key rows of HD 16-bit elements), conflict-free on the 64-bank LDS:
+//  * K: the 16-byte chunk c of key row r sits at chunk c ^ k_swizzle(r). A fragment's 16-lane group
+//    reads one chunk of 16 consecutive rows: with 256-byte rows (HD 128) the XOR with r & 15 spreads
+//    them over the 16 positions; with 128-byte rows (HD 64) two rows share 256 bytes, and the XOR
+//    with (r / 2) & 7 spreads the 8 row pairs.
+//  * V: the 32-byte unit u of key row r sits at unit u ^ v_swizzle(r). A 32-lane half of a transposed
+//    read covers units (u, u ^ 1) of four consecutive rows: 256-byte rows use gemm::tr_swizzle
+//    (2 (r & 3)); 128-byte rows (4 units, two rows per 256 bytes) XOR with 2 ((r / 2) & 1).
+template <int HD> __device__ __forceinline__ int k_swizzle(int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); }
+template <int HD> __device__ __forceinline__ int v_swizzle(int r) { return HD == 128 ? gemm::tr_swizzle(r) : 2 * ((r >> 1) & 1); }
+
+// Issues this wave's share of the K tile of keys [k0, k0 + 32): HD / 16 instructions of 1 KiB.
+template <int WAVES, long KS, int HD>
 __device__ __forceinline__ void load_k(const u16_t* __restrict__ kb, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int PER = 8 / WAVES;
+  constexpr int PER = HD / 16 / WAVES, LPR = HD / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int gi = wave * PER + i;
-    const int row = 4 * gi + (lane >> 4);
-    const int c = (lane & 15) ^ (row & 15);
+    const int row = RPI * gi + lane / LPR;
+    const int c = (lane % LPR) ^ k_swizzle<HD>(row);
     gemm::dma16(kb + (k0 + row) * KS + 8 * c, (ACCY_LDS void*)(lds + gi * 512));
   }
 }
 
-template <int WAVES, long VS>
+template <int WAVES, long VS, int HD>
 __device__ __forceinline__ void load_v(const u16_t* __restrict__ vb, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int PER = 8 / WAVES;
+  constexpr int PER = HD / 16 / WAVES, LPR = HD / 8, RPI = 64 / LPR;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int gi = wave * PER + i;
-    const int row = 4 * gi + (lane >> 4);
-    const int p = lane & 15;
-    const int u = (p >> 1) ^ gemm::tr_swizzle(row);
+    const int row = RPI * gi + lane / LPR;
+    const int p = lane % LPR;
+    const int u = (p >> 1) ^ v_swizzle<HD>(row);
     gemm::dma16(vb + (k0 + row) * VS + 16 * u + 8 * (p & 1), (ACCY_LDS void*)(lds + gi * 512));
   }
 }
 
 // A operand of S^T for the block's 32 keys and head-dim step dd (16 elements).
+template <int HD>
 __device__ __forceinline__ u32x4 k_frag(const u16_t* lds, int dd, int lane) {
   const int row = lane & 31;
   const int c = 2 * dd + (lane >> 5);
-  return *(const u32x4*)(lds + row * HD + ((c ^ (row & 15)) << 3));
+  return *(const u32x4*)(lds + row * HD + ((c ^ k_swizzle<HD>(row)) << 3));
 }
 
 // A operand of O^T = V^T P^T for head-dim tile dt (32) and 16-key step s, keys in the permuted order.
+template <int HD>
 __device__ __forceinline__ u32x4 v_frag(const u16_t* lds, int dt, int s, int lane) {
   const int g = lane >> 4, i = lane & 15;
   const int n0 = dt * 32 + ((g & 1) << 4);
@@ -101,7 +114,7 @@ __device__ __forceinline__ u32x4 v_frag(const u16_t* lds, int dt, int s, int lan
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int k = 16 * s + 8 * r + 4 * (g >> 1) + (i >> 2);
-    const int unit = (n0 >> 4) ^ gemm::tr_swizzle(k);
+    const int unit = (n0 >> 4) ^ v_swizzle<HD>(k);
     const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ACCY_LDS i16x4*)(lds + k * HD + unit * 16 + 4 * (i & 3)));
     out[2 * r] = (u32_t)(u16_t)v[0] | ((u32_t)(u16_t)v[1] << 16);
     out[2 * r + 1] = (u32_t)(u16_t)v[2] | ((u32_t)(u16_t)v[3] << 16);
@@ -203,8 +216,9 @@ struct Lds {
 
 template <class C>
 struct Scorer {
-  static constexpr int WAVES = C::WAVES, QT = 2, DS = HD / 16;
-  static constexpr int PER = 8 / WAVES;  // K load instructions per wave per key block
+  static constexpr int HD = C::HD, WAVES = C::WAVES, QT = 2, DS = HD / 16;
+  static constexpr int NS = QT * DS;            // score MFMAs per key block (16 for HD 128, 8 for HD 64)
+  static constexpr int PER = HD / 16 / WAVES;  // K load instructions per wave per key block
   static constexpr long NQB = C::SQ / (64 * WAVES), NKB = C::SK / BK;
 
   Lds<C> sh;
@@ -290,14 +304,16 @@ struct Scorer {
       s[SB][qt] = f32x16{};
     }
     if constexpr (PREV && C::CAUSAL) mask<PB>(kprev0);
-    u32x4 a = k_frag(kl, 0, lane), an = a;
-    For<0, 16>::run([&](auto ti) {
+    u32x4 a = k_frag<HD>(kl, 0, lane), an = a;
+    For<0, NS>::run([&](auto ti) {
       constexpr int t = decltype(ti)::value, dd = t >> 1, qt = t & 1;
-      if constexpr (qt == 0 && t + 2 < 16) an = k_frag(kl, (t + 2) >> 1, lane);
+      if constexpr (qt == 0 && t + 2 < NS) an = k_frag<HD>(kl, (t + 2) >> 1, lane);
       s[SB][qt] = gemm::mfma32x32x16<C::DT>(a, qf[qt][dd], s[SB][qt]);
       if constexpr (qt == 1) a = an;
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (PREV) softmax_slot<PB, t>(mx, msub, ls, p, alpha);
+      // the 16 softmax slots of the previous block, spread over this block's NS MFMAs
+      if constexpr (PREV)
+        For<t * 16 / NS, (t + 1) * 16 / NS>::run([&](auto si) { softmax_slot<PB, decltype(si)::value>(mx, msub, ls, p, alpha); });
       __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (PREV) {
@@ -341,7 +357,7 @@ struct Scorer {
     if (t + 1 < nkb) gemm::wait_vmcnt<PER>();
     else gemm::wait_vmcnt<0>();
     gemm::lds_reads_done_barrier();
-    if (t + 2 < nkb) load_k<WAVES, C::K_S>(kb, (t + 2) * BK, sh.ks[(ST + 2) & 3], wave, lane);
+    if (t + 2 < nkb) load_k<WAVES, C::K_S, HD>(kb, (t + 2) * BK, sh.ks[(ST + 2) & 3], wave, lane);
     u32x4 p[QT][2];
     float alpha[QT];
     scores<ST, ST & 1, (ST + 1) & 1, true>((t - 1) * BK, p, alpha);
@@ -368,13 +384,13 @@ struct Scorer {
       m[qt] = -__builtin_inff();
       l[qt] = 0.0f;
     }
-    load_k<WAVES, C::K_S>(kb, 0, sh.ks[0], wave, lane);
-    if (nkb > 1) load_k<WAVES, C::K_S>(kb, BK, sh.ks[1], wave, lane);
+    load_k<WAVES, C::K_S, HD>(kb, 0, sh.ks[0], wave, lane);
+    if (nkb > 1) load_k<WAVES, C::K_S, HD>(kb, BK, sh.ks[1], wave, lane);
     // Step 0: scores of block 0 only.
     if (nkb > 1) gemm::wait_vmcnt<PER>();
     else gemm::wait_vmcnt<0>();
     gemm::lds_reads_done_barrier();
-    if (nkb > 2) load_k<WAVES, C::K_S>(kb, 2 * BK, sh.ks[2], wave, lane);
+    if (nkb > 2) load_k<WAVES, C::K_S, HD>(kb, 2 * BK, sh.ks[2], wave, lane);
     {
       u32x4 unused_p[QT][2];
       float unused_a[QT];
@@ -401,8 +417,9 @@ struct Scorer {
 
 template <class C>
 struct Accumulator {
-  static constexpr int WAVES = C::WAVES, QT = 2, DTN = HD / 32;
-  static constexpr int PER = 8 / WAVES;  // V load instructions per wave per key block
+  static constexpr int HD = C::HD, WAVES = C::WAVES, QT = 2, DTN = HD / 32;
+  static constexpr int NA = DTN * 2 * QT;      // P.V MFMAs per key block (16 for HD 128, 8 for HD 64)
+  static constexpr int PER = HD / 16 / WAVES;  // V load instructions per wave per key block
 
   Lds<C> sh;
   const u16_t* __restrict__ vb;
@@ -427,7 +444,7 @@ struct Accumulator {
 #pragma unroll
     for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
-      for (int st = 0; st < 2; ++st) vf[dt][st] = v_frag(vl, dt, st, lane);
+      for (int st = 0; st < 2; ++st) vf[dt][st] = v_frag<HD>(vl, dt, st, lane);
     if (__any(al.x != 1.0f || al.y != 1.0f)) {
 #pragma unroll
       for (int dt = 0; dt < DTN; ++dt) {
@@ -435,7 +452,7 @@ struct Accumulator {
         o[1][dt] *= al.y;
       }
     }
-    For<0, 16>::run([&](auto ti) {
+    For<0, NA>::run([&](auto ti) {
       constexpr int t = decltype(ti)::value, dt = t >> 2, st = (t >> 1) & 1, qt = t & 1;
       o[qt][dt] = gemm::mfma32x32x16<C::DT>(vf[dt][st], p[qt][st], o[qt][dt]);
     });
@@ -447,7 +464,7 @@ struct Accumulator {
     if (t - 1 < nkb) gemm::wait_vmcnt<PER>();
     else gemm::wait_vmcnt<0>();
     gemm::lds_reads_done_barrier();
-    if (t < nkb) load_v<WAVES, C::V_S>(vb, t * BK, sh.vs[ST], wave, lane);
+    if (t < nkb) load_v<WAVES, C::V_S, HD>(vb, t * BK, sh.vs[ST], wave, lane);
     consume<ST & 1, (ST + 2) & 3>();
   }
 
@@ -458,9 +475,9 @@ struct Accumulator {
       for (int dt = 0; dt < DTN; ++dt) o[qt][dt] = f32x16{};
     // Steps 0 and 1: V(0) and V(1) are issued.
     gemm::lds_reads_done_barrier();
-    load_v<WAVES, C::V_S>(vb, 0, sh.vs[0], wave, lane);
+    load_v<WAVES, C::V_S, HD>(vb, 0, sh.vs[0], wave, lane);
     gemm::lds_reads_done_barrier();
-    if (nkb > 1) load_v<WAVES, C::V_S>(vb, BK, sh.vs[1], wave, lane);
+    if (nkb > 1) load_v<WAVES, C::V_S, HD>(vb, BK, sh.vs[1], wave, lane);
     // Steps 2 .. nkb + 1.
     long t = 2;
     for (; t + 3 <= nkb + 1; t += 4) {
@@ -541,9 +558,10 @@ __device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __res
 template <class C>
 __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
                                       const u16_t* __restrict__ V, u16_t* __restrict__ O) {
-  constexpr int WAVES = C::WAVES, QT = 2;
+  constexpr int WAVES = C::WAVES, QT = 2, HD = C::HD;
   constexpr long BQ = 64 * WAVES, NQB = C::SQ / BQ, PAIR = blocks_per_group<C>(), PER_B = NQB / PAIR;
   static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
+  static_assert((HD == 64 || HD == 128) && (HD / 16) % WAVES == 0, "head dimension 64 or 128");
   __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
   __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
   __shared__ __attribute__((aligned(16))) u32x4 pbuf[2 * WAVES * QT * 2 * 64];
@@ -567,6 +585,154 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   } else {
     flash_block<C>(sh, Q, K, V, O, b, C::CAUSAL ? NQB - 1 - p : p);
   }
+}
+
+// ---------------------------------------------------------------------------------------------
+// f32 attention with a head dimension of 64: the reference's own flash pattern (f32 Q, K, V of head
+// dimension 64, src/preparation/kernelization/lowering/flash.zig:24-31), on v_mfma_f32_32x32x2_f32.
+//
+// A workgroup of WAVES waves owns 32 * WAVES queries of one batch index; each wave keeps its 32
+// queries' Q^T in registers and streams the keys in blocks of 32 through two LDS buffers. Lane half
+// h = lane / 32 supplies head dims 32 h .. 32 h + 31 to both MFMA operands (any split of the
+// contracted dims is valid when A and B agree), so one ds_read_b128 of a K row feeds four MFMAs.
+// Per block of 32 keys:
+//  * S^T = K Q^T: 32 MFMAs into one 32 x 32 accumulator (lane l: query l % 32, keys 8 g + 4 h + j in
+//    register 4 g + j);
+//  * online softmax in f32 in the log2 domain: the scores are scaled by SL = scale * log2 e, the
+//    block maximum joins the running maximum (exchange with lane l ^ 32, which holds the same query),
+//    O and the row sum are rescaled by exp2(m_old - m_new) every block;
+//  * O^T += V^T P^T: two head-dim tiles x 16 key steps; step (g, j) takes key 8 g + j from lanes
+//    0-31 and key 8 g + 4 + j from lanes 32-63, exactly the keys those lanes' score registers 4 g + j
+//    hold, so P is the B operand as it stands; V is stored transposed in LDS so that one
+//    ds_read_b128 gives the A operands of four steps;
+// then O = O / l. LDS layouts (conflict-free 16-lane b128 reads on the 64-bank LDS): K as [key][64]
+// with the 16-byte chunk c of key row r at chunk c ^ (r & 15); V^T as [64][32 keys] with the chunk of
+// keys 4 kc .. 4 kc + 3 of row d at chunk kc ^ ((d / 2) & 7).
+// The configuration struct C supplies WAVES, SQ, SK, NB, Q_S, K_S, V_S (element strides of a query /
+// key row; head dims have stride 1), CAUSAL, SL and q_off / k_off / v_off (batch offsets). O is
+// written row-major as [b][q][64]. Launched with 64 * WAVES threads, NB * SQ / (32 * WAVES) workgroups.
+template <class C>
+__device__ __forceinline__ void flash_f32(const float* __restrict__ Q, const float* __restrict__ K,
+                                          const float* __restrict__ V, float* __restrict__ O) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  constexpr int WAVES = C::WAVES, D = 64, THREADS = 64 * WAVES, LD = 512 / THREADS;
+  constexpr long BQ = 32 * WAVES, NQB = C::SQ / BQ;
+  static_assert(C::SQ % BQ == 0 && C::SK % 32 == 0 && 512 % THREADS == 0, "exact blocks only");
+  __shared__ __attribute__((aligned(16))) float ks[2][32 * D];
+  __shared__ __attribute__((aligned(16))) float vt[2][D * 32];
+
+  // Workgroups of one batch index go to one XCD (they share its K and V); under a causal mask the
+  // query blocks with the most keys start first.
+  const long total = (long)gridDim.x;
+  long t = (long)blockIdx.x;
+  if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+  const long b = t / NQB, qb = C::CAUSAL ? NQB - 1 - t % NQB : t % NQB;
+  if (b >= C::NB) return;  // a grid larger than the work
+  const int tid = (int)threadIdx.x, wave = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const long q0 = qb * BQ, query = q0 + 32 * wave + l32;
+  const float* __restrict__ qp = Q + C::q_off(b);
+  const float* __restrict__ kp = K + C::k_off(b);
+  const float* __restrict__ vp = V + C::v_off(b);
+
+  float qf[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f32x4 x = *(const f32x4*)(qp + query * C::Q_S + 32 * h + 4 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qf[4 * i + e] = x[e];
+  }
+  long nkb = C::SK / 32;
+  if constexpr (C::CAUSAL) {
+    const long last = (q0 + BQ - 1) / 32 + 1;
+    nkb = last < nkb ? last : nkb;
+  }
+
+  // A block's K and V tiles (32 x 64 f32 each, 512 16-byte chunks): LD chunks of each per thread.
+  f32x4 kr[LD], vr[LD];
+  auto fetch = [&](long k0) {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int idx = tid + i * THREADS, row = idx >> 4, c = idx & 15;
+      kr[i] = *(const f32x4*)(kp + (k0 + row) * C::K_S + 4 * c);
+      vr[i] = *(const f32x4*)(vp + (k0 + row) * C::V_S + 4 * c);
+    }
+  };
+  auto stash = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int idx = tid + i * THREADS, row = idx >> 4, c = idx & 15;
+      *(f32x4*)(&ks[buf][row * D + 4 * (c ^ (row & 15))]) = kr[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = 4 * c + e;
+        vt[buf][d * 32 + 4 * ((row >> 2) ^ ((d >> 1) & 7)) + (row & 3)] = vr[i][e];
+      }
+    }
+  };
+
+  float m = -__builtin_inff(), l = 0.0f;
+  f32x16 o[2] = {f32x16{}, f32x16{}};
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (long j = 0; j < nkb; ++j) {
+    const int buf = (int)(j & 1);
+    if (j + 1 < nkb) fetch((j + 1) * 32);
+    const float* kl = ks[buf];
+    const float* vl = vt[buf];
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 a = *(const f32x4*)(kl + l32 * D + 4 * ((8 * h + i) ^ (l32 & 15)));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = gemm::mfma32x32x2f32(a[e], qf[4 * i + e], s);
+    }
+    const long k0 = j * 32;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float x = s[r] * C::SL;
+      if constexpr (C::CAUSAL) {
+        if (k0 + 8 * (r >> 2) + 4 * h + (r & 3) > query) x = -__builtin_inff();
+      }
+      s[r] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);
+    const float msub = mn == -__builtin_inff() ? 0.0f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - msub);
+    float ps = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = __builtin_amdgcn_exp2f(s[r] - msub);
+      ps += s[r];
+    }
+    l = l * alpha + ps;
+    m = mn;
+    o[0] *= alpha;
+    o[1] *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d = dt * 32 + l32;
+        const f32x4 a = *(const f32x4*)(vl + d * 32 + 4 * ((2 * g + h) ^ ((d >> 1) & 7)));
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) o[dt] = gemm::mfma32x32x2f32(a[jj], s[4 * g + jj], o[dt]);
+      }
+    // Buffer (j + 1) % 2 was last read in block j - 1, before the barrier that ended it.
+    if (j + 1 < nkb) stash((int)((j + 1) & 1));
+    __syncthreads();
+  }
+  const float inv = 1.0f / (l + __shfl_xor(l, 32, 64));
+  float* __restrict__ orow = O + (b * C::SQ + query) * D;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *(f32x4*)(orow + dt * 32 + 8 * g + 4 * h) =
+          f32x4{o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv};
 }
 
 }  // namespace attn

@@ -1467,7 +1467,7 @@ class Planner {
   bool match_attention(uint32_t pv, Attn& at) const {
     const Op& d = g_.ops[pv];
     const DType dt = d.result.dtype;
-    if (d.kind != Kind::dot_general || (dt != DType::f16 && dt != DType::bf16)) return false;
+    if (d.kind != Kind::dot_general || (dt != DType::f16 && dt != DType::bf16 && dt != DType::f32)) return false;
     const uint32_t pdiv = d.args[0];
     const Op& dv = g_.ops[pdiv];
     const size_t R = dv.result.rank();
@@ -1555,7 +1555,7 @@ class Planner {
   }
 
   struct AttnLayout {
-    int64_t sq = 0, sk = 0, nb = 1, q_s = 0, k_s = 0, v_s = 0;
+    int64_t sq = 0, sk = 0, nb = 1, q_s = 0, k_s = 0, v_s = 0, hd = 0;
     std::vector<int64_t> extents, q_b, k_b, v_b;  // batch axes: extents and per-operand strides
     View q, k, v;
   };
@@ -1583,15 +1583,23 @@ class Planner {
     const int vf = free_axis(vt.rank(), d.rhs_batch, d.rhs_contract);
     if (qf < 0 || kf < 0 || vf < 0 || d.rhs_contract.size() != 1) return false;
     const size_t qc = (size_t)qk.lhs_contract[0], kc = (size_t)qk.rhs_contract[0], vc = (size_t)d.rhs_contract[0];
-    if (qt.dims[qc].extent != 128 || kt.dims[kc].extent != 128 || vt.dims[(size_t)vf].extent != 128) return false;
+    // Head dimension (Q.K contraction and V's free axis, unit stride): 64 or 128 for 16-bit operands
+    // (attn::flash), 64 for f32 (attn::flash_f32, the reference's flash pattern).
+    const bool f32 = d.result.dtype == DType::f32;
+    L.hd = qt.dims[qc].extent;
+    if ((L.hd != 128 || f32) && L.hd != 64) return false;
+    if (kt.dims[kc].extent != L.hd || vt.dims[(size_t)vf].extent != L.hd) return false;
     if (L.q.strides[qc] != 1 || L.k.strides[kc] != 1 || L.v.strides[(size_t)vf] != 1) return false;
     L.sq = qt.dims[(size_t)qf].extent;
     L.sk = kt.dims[(size_t)kf].extent;
-    if (vt.dims[vc].extent != L.sk || L.sq % 64 != 0 || L.sk % 64 != 0 || L.sq == 0 || L.sk == 0) return false;
+    const int64_t qmul = f32 ? 32 : 64, kmul = f32 ? 32 : 64;
+    if (vt.dims[vc].extent != L.sk || L.sq % qmul != 0 || L.sk % kmul != 0 || L.sq == 0 || L.sk == 0) return false;
     L.q_s = L.q.strides[(size_t)qf];
     L.k_s = L.k.strides[(size_t)kf];
     L.v_s = L.v.strides[vc];
-    auto ok8 = [](int64_t x) { return x % 8 == 0; };
+    // 16-byte aligned rows and batch offsets (8 16-bit or 4 f32 elements)
+    const int64_t al = f32 ? 4 : 8;
+    auto ok8 = [al](int64_t x) { return x % al == 0; };
     if (!ok8(L.q_s) || !ok8(L.k_s) || !ok8(L.v_s) || !ok8(L.q.offset) || !ok8(L.k.offset) || !ok8(L.v.offset)) return false;
     for (size_t i = 0; i < qk.lhs_batch.size(); ++i) {
       const int64_t e = qt.dims[(size_t)qk.lhs_batch[i]].extent;
@@ -1624,8 +1632,13 @@ class Planner {
   void attention(uint32_t pv, const Attn& at, const AttnLayout& L) {
     const Op& d = g_.ops[pv];
     const DType dt = d.result.dtype;
+    if (dt == DType::f32) {
+      attention_f32(pv, at, L);
+      return;
+    }
     int out = slots_.slot_of[pv] >= 0 ? slots_.slot_of[pv] : temp_slot(pv);
-    const int waves = L.sq % 256 == 0 ? 4 : (L.sq % 128 == 0 ? 2 : 1);
+    // waves per role: every role's share of a K / V tile (HD / 16 load instructions) must be whole
+    const int waves = L.sq % 256 == 0 && L.hd / 16 % 4 == 0 ? 4 : (L.sq % 128 == 0 ? 2 : 1);
     KernelWriter w(g_, slots_, "i64_t");
     std::string q = w.arg(L.q.slot, false), k = w.arg(L.k.slot, false), v = w.arg(L.v.slot, false),
                 o = w.arg(out, true);
@@ -1635,7 +1648,8 @@ class Planner {
     std::ostringstream src;
     src << kMfmaVgprForm << "#include \"gemm\"\n#include \"attention\"\n";
     src << "struct Cfg_" << nm << " {\n"
-        << "  static constexpr int DT = " << (dt == DType::bf16 ? 0 : 1) << ", WAVES = " << waves << ";\n"
+        << "  static constexpr int DT = " << (dt == DType::bf16 ? 0 : 1) << ", HD = " << L.hd << ", WAVES = " << waves
+        << ";\n"
         << "  static constexpr long SQ = " << L.sq << ", SK = " << L.sk << ", NB = " << L.nb << ";\n"
         << "  static constexpr long Q_S = " << L.q_s << ", K_S = " << L.k_s << ", V_S = " << L.v_s << ";\n"
         << "  static constexpr bool CAUSAL = " << (at.causal ? "true" : "false") << ";\n"
@@ -1666,16 +1680,65 @@ class Planner {
     ks.block[0] = 128 * waves;  // a scorer and an accumulator wave per 64 queries
     ks.klass = "attention";
     ks.label = "attention:%" + std::to_string(pv);
-    // Score pairs actually needed: all of them, or those with key <= query under the causal mask.
+    ks.algorithmic_flops = 4.0 * (double)L.nb * attention_pairs(at, L) * (double)L.hd;
+    push(std::move(ks), w);
+    finish(pv);
+  }
+
+  // Score pairs the kernel computes: all of them, or those with key <= query under the causal mask.
+  static double attention_pairs(const Attn& at, const AttnLayout& L) {
     double pairs = (double)L.sq * (double)L.sk;
     if (at.causal) {
       const double n = (double)std::min(L.sq, L.sk);
       pairs = n * (n + 1) / 2 + (L.sq > L.sk ? (double)(L.sq - L.sk) * (double)L.sk : 0.0);
     }
-    ks.algorithmic_flops = 4.0 * (double)L.nb * pairs * 128.0;
+    return pairs;
+  }
+
+  // f32 attention of head dimension 64 (attn::flash_f32): 32 queries per wave.
+  void attention_f32(uint32_t pv, const Attn& at, const AttnLayout& L) {
+    int out = slots_.slot_of[pv] >= 0 ? slots_.slot_of[pv] : temp_slot(pv);
+    const int waves = L.sq % 128 == 0 ? 4 : (L.sq % 64 == 0 ? 2 : 1);
+    KernelWriter w(g_, slots_, "i64_t");
+    std::string q = w.arg(L.q.slot, false), k = w.arg(L.k.slot, false), v = w.arg(L.v.slot, false),
+                o = w.arg(out, true);
+    std::string nm = name("attention", pv);
+    char sl[64];
+    std::snprintf(sl, sizeof sl, "%af", (double)(float)(at.scale * 1.4426950408889634));
+    std::ostringstream src;
+    src << "#include \"gemm\"\n#include \"attention\"\n";
+    src << "struct Cfg_" << nm << " {\n"
+        << "  static constexpr int WAVES = " << waves << ";\n"
+        << "  static constexpr long SQ = " << L.sq << ", SK = " << L.sk << ", NB = " << L.nb << ";\n"
+        << "  static constexpr long Q_S = " << L.q_s << ", K_S = " << L.k_s << ", V_S = " << L.v_s << ";\n"
+        << "  static constexpr bool CAUSAL = " << (at.causal ? "true" : "false") << ";\n"
+        << "  static constexpr float SL = " << sl << ";\n"
+        << "  static __device__ __forceinline__ long q_off(long b) { return " << batch_offset(L.extents, L.q_b, L.q.offset)
+        << "; }\n"
+        << "  static __device__ __forceinline__ long k_off(long b) { return " << batch_offset(L.extents, L.k_b, L.k.offset)
+        << "; }\n"
+        << "  static __device__ __forceinline__ long v_off(long b) { return " << batch_offset(L.extents, L.v_b, L.v.offset)
+        << "; }\n};\n";
+    std::string params;
+    for (const std::string& x : {q, k, v}) {
+      if (params.find("* __restrict__ " + x + ",") != std::string::npos) continue;
+      params += "const float* __restrict__ " + x + ", ";
+    }
+    params += "float* __restrict__ " + o;
+    src << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << nm << "(" << params
+        << ") {\n  accy::attn::flash_f32<Cfg_" << nm << ">(" << q << ", " << k << ", " << v << ", " << o << ");\n}\n";
+    KernelStep ks;
+    ks.source = src.str();
+    ks.name = nm;
+    ks.grid[0] = (uint32_t)(L.nb * (L.sq / (32 * waves)));
+    ks.block[0] = 64 * waves;
+    ks.klass = "attention";
+    ks.label = "attention:%" + std::to_string(pv);
+    ks.algorithmic_flops = 4.0 * (double)L.nb * attention_pairs(at, L) * (double)L.hd;
     push(std::move(ks), w);
     finish(pv);
   }
+
 
   void dot(uint32_t v) {
     const Op& op = g_.ops[v];

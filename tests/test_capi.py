@@ -55,15 +55,19 @@ def test_every_config_program_lowers_and_compiles_for_gfx950(name):
     (lambda: W.attention_program(32, 4096, 128, "f16"), True),
     (lambda: W.attention_program(2, 384, 128, "bf16", causal=True), True),
     (lambda: W.decoder_program(), True),
-    (lambda: W.attention_program(2, 128, 64), False),     # head dimension 64: unfused kernels
+    (lambda: W.attention_program(2, 128, 64), True),      # head dimension 64 (16-bit)
     (lambda: W.attention_program(2, 96, 128), False),     # 96 queries: not a multiple of 64
+    (lambda: W.attention_program(2, 256, 256), False),    # head dimension 256: unfused kernels
+    (lambda: W.attention_program(2, 128, 64, "f32"), True),          # the reference's flash pattern
+    (lambda: W.attention_program(1, 96, 64, "f32", causal=True), True),
+    (lambda: W.attention_program(2, 128, 128, "f32"), False),        # f32 fuses at head dimension 64
 ])
 def test_attention_fusion_decision(prog, fused):
     src = hip.plan_source(prog(), compile=False)
     assert ("accy::attn::flash" in src) == fused
     if fused:
-        # scores, softmax and the product with V in one kernel: no 16-bit score buffer is planned
-        assert src.count("accy::attn::flash<") == 1
+        # scores, softmax and the product with V in one kernel: no score buffer is planned
+        assert src.count("accy::attn::flash<") + src.count("accy::attn::flash_f32<") == 1
 
 
 def test_attention_fusion_keeps_values_read_elsewhere():

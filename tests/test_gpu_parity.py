@@ -372,10 +372,38 @@ def test_gemm_f32_other_layouts_repacked_onto_mfma(case):
 
 
 def test_f32_attention_scores_on_the_matrix_cores():
-    prog = W.attention_program(4, 1024, 64, "f32")
-    assert "accy::gemm::mma32f<" in hip.plan_source(prog)
-    ins = W.attention_inputs(4, 1024, 64, "f32", seed=12)
+    # head dimension 128 in f32 is not fused: the scores and P.V run on the f32 MFMA contraction
+    prog = W.attention_program(2, 1024, 128, "f32")
+    src = hip.plan_source(prog)
+    assert "accy::gemm::mma32f<" in src and "accy::attn::" not in src
+    ins = W.attention_inputs(2, 1024, 128, "f32", seed=12)
     assert_normwise(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 1e-3, "f32")
+
+
+@pytest.mark.parametrize("heads,seq,causal", [(4, 1024, False), (3, 512, True), (2, 96, True), (1, 224, False)])
+def test_fused_f32_attention_head_dim_64(heads, seq, causal):
+    """The reference's own flash pattern (f32, head dimension 64; lowering/flash.zig:24-31) runs as one
+    fused kernel (attn::flash_f32): within BASELINE's f32 attention bound (1e-3 normwise and per
+    element with a floor) of runCpu's per-op f32 evaluation, and of the float64 formula."""
+    say(f"f32 attention {heads} x {seq} x 64 causal={causal}")
+    prog = W.attention_program(heads, seq, 64, "f32", causal=causal)
+    assert "accy::attn::flash_f32<" in hip.plan_source(prog)
+    ins = W.attention_inputs(heads, seq, 64, "f32", seed=heads + seq)
+    got = hip_run(prog, ins)[0]
+    assert_normwise(got, oracle_run(prog, ins)[0], 1e-3, "f32")
+    exact = exact_attention(*ins, 1.0 / math.sqrt(64), causal, "f32")
+    assert np.abs(got - exact).max() <= 1e-4 * np.abs(exact).max()
+
+
+@pytest.mark.parametrize("heads,seq,dtype,causal", [(2, 512, "bf16", False), (3, 256, "f16", True), (2, 128, "f16", False)])
+def test_fused_16bit_attention_head_dim_64(heads, seq, dtype, causal):
+    say(f"{dtype} attention {heads} x {seq} x 64 causal={causal}")
+    prog = W.attention_program(heads, seq, 64, dtype, causal=causal)
+    assert "accy::attn::flash<" in hip.plan_source(prog)
+    ins = W.attention_inputs(heads, seq, 64, dtype, seed=3 * heads + seq)
+    scale = float(to_f32(W.to_dtype(np.array([1 / math.sqrt(64)]), dtype), dtype)[0])
+    assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype,
+                     exact_attention(*ins, scale, causal, dtype))
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])

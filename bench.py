@@ -12,8 +12,10 @@
   program, around that kernel in each of K back-to-back steps otherwise. ``traffic`` is the HBM
   bytes per launch measured with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, calibrated on a copy
   kernel) and committed in profiles/traffic.json; null for a workload not measured there.
-* ``cpu_baseline`` is the CPU oracle (the runCpu restatement, oracle/) timed on this host on a
-  bounded sample of the same workload, then scaled to the metric's unit (kind "port").
+* ``cpu_baseline`` is the runCpu restatement (oracle/) timed on this host on a bounded sample of the
+  same workload, then scaled to the metric's unit (kind "port"): for C1-C4 runCpu's kernel plan as
+  fused loops (oracle/runcpu_plan.cpp), for C5 the op-by-op oracle; all host threads (at most 16)
+  and one thread.
 
 The headline workload is C2 (row-wise logsumexp, x f32[32768, 8192]), the configuration the metric
 is quoted on that fits one GPU: ``value``, ``roofline`` and ``cpu_baseline`` are C2's. The default run
@@ -148,14 +150,54 @@ def cpu_threads() -> int:
     return min(int(os.environ.get("ACCY_CPU_THREADS", "0")) or (os.cpu_count() or 1), 16)
 
 
-def oracle_time(cfg, budget_s: float):
-    """Times the CPU oracle on the config's bounded sample, with all host threads and with one thread
-    (runCpu launches single-threaded); each leg until `budget_s` is spent (at most 50 runs). The
-    oracle's per-output order makes both legs bit-identical."""
+def plan_runner(name: str, lib, prog, ins):
+    """The CPU baseline's computation for one config: runCpu's kernel plan as fused loops
+    (oracle/runcpu_plan.cpp: no intermediate is materialised; each output's arithmetic is the op-by-op
+    oracle's, which tests/test_cpu_plan.py checks bit for bit) for C1-C4, the op-by-op oracle
+    otherwise. Returns (callable, description)."""
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    ptr = lambda x: ctypes.c_void_p(x.ctypes.data)
+    if name == "c1-tone":
+        f, t, s = ins
+        out = np.zeros(f.shape[0], np.float32)
+        lib.accy_cpu_plan_tone.argtypes = [vp, i64, vp, vp, i64, vp]
+        return (lambda: lib.accy_cpu_plan_tone(ptr(f), f.shape[0], ptr(t), ptr(s), t.shape[0], ptr(out)),
+                "fused reduction (runCpu's plan)")
+    if name == "c2-lse":
+        x = ins[0]
+        out = np.zeros(x.shape[0], np.float32)
+        lib.accy_cpu_plan_logsumexp.argtypes = [vp, i64, i64, vp]
+        return (lambda: lib.accy_cpu_plan_logsumexp(ptr(x), x.shape[0], x.shape[1], ptr(out)),
+                "max reduction, fused exp-sum reduction, log + add (runCpu's plan)")
+    if name in ("c3-gemm-f32", "c3-gemm-bf16"):
+        a, b = ins
+        out = np.zeros((a.shape[0], b.shape[1]), a.dtype)
+        lib.accy_cpu_plan_mulsum.argtypes = [vp, vp, i64, i64, i64, ctypes.c_int, vp]
+        bf = int(name.endswith("bf16"))
+        return (lambda: lib.accy_cpu_plan_mulsum(ptr(a), ptr(b), a.shape[0], a.shape[1], b.shape[1], bf, ptr(out)),
+                "interior reduction of rounded products, serial k (runCpu's plan)")
+    if name == "c4-attention":
+        q, k, v = ins
+        out = np.zeros_like(q)
+        scale = int(np.array([1.0 / math.sqrt(q.shape[2])], np.float16).view(np.uint16)[0])
+        lib.accy_cpu_plan_attention_f16.argtypes = [vp, vp, vp, i64, i64, i64, ctypes.c_uint16, ctypes.c_int, vp]
+        return (lambda: lib.accy_cpu_plan_attention_f16(ptr(q), ptr(k), ptr(v), q.shape[0], q.shape[1], q.shape[2],
+                                                         scale, 0, ptr(out)),
+                "per query row: scores, per-op f16 softmax, P.V (runCpu's operations, f16 extension)")
     sys.path.insert(0, str(ROOT / "tests"))
-    from conftest import oracle_lib, oracle_run
+    from conftest import oracle_run
+    return (lambda: oracle_run(prog, ins)), "op-by-op oracle (every intermediate materialised)"
+
+
+def oracle_time(name: str, cfg, budget_s: float):
+    """Times the CPU baseline on the config's bounded sample, with all host threads and with one
+    thread (runCpu launches single-threaded); each leg until `budget_s` is spent (at most 50 runs).
+    Per-output order makes both legs bit-identical."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    from conftest import oracle_lib
     prog, ins, work = cfg["sample"]()
     lib = oracle_lib()
+    run, plan = plan_runner(name, lib, prog, ins)
     threads = cpu_threads()
     scale = 1e9 if cfg["unit"] in ("GB/s", "GFLOP/s") else 1e12
 
@@ -165,7 +207,7 @@ def oracle_time(cfg, budget_s: float):
         start = time.perf_counter()
         while True:
             t0 = time.perf_counter()
-            oracle_run(prog, ins)
+            run()
             times.append(time.perf_counter() - t0)
             if time.perf_counter() - start >= budget_s or len(times) >= 50:
                 break
@@ -174,7 +216,7 @@ def oracle_time(cfg, budget_s: float):
     t_all, n_all = timed(threads)
     t_one, n_one = timed(1)
     lib.accy_cpu_set_threads(threads)
-    return dict(value=work / t_all / scale, unit=cfg["unit"], cores=threads, kind="port",
+    return dict(value=work / t_all / scale, unit=cfg["unit"], cores=threads, kind="port", plan=plan,
                 sample=f"{cfg['sample_desc']}; median of {n_all} runs, {t_all:.3f} s each",
                 single_core=dict(value=work / t_one / scale, cores=1,
                                  sample=f"median of {n_one} runs, {t_one:.3f} s each"))
@@ -294,7 +336,7 @@ def main() -> int:
         print(f"bench: {name}", file=sys.stderr, flush=True)
         r = measure(name, cfgs[name], args.steps, args.warmup, args.warmup_seconds)
         budget = args.cpu_budget if name == head else args.cpu_budget / 3
-        r["cpu_baseline"] = None if args.no_cpu else oracle_time(cfgs[name], budget)
+        r["cpu_baseline"] = None if args.no_cpu else oracle_time(name, cfgs[name], budget)
         results[name] = r
     h = results[head]
     line = {

@@ -2,22 +2,18 @@
 // gfx950 matrix cores, for 16-bit Q, K, V with a head dimension HD of 64 or 128 (both for Q.K and for
 // V), and (flash_f32, at the end) for f32 Q, K, V with a head dimension of 64.
 //
-// A workgroup of 2 * WAVES wavefronts owns 64 * WAVES queries of one batch index and streams the
-// keys in blocks of 32. Each group of 64 queries (two 32-query tiles, q0 + 32 w and
-// q0 + 32 (WAVES + w), so that under a causal mask every group has almost the same work) is served
-// by a scorer wave (S and softmax) and an accumulator wave (P.V and the output); see the work split
-// below.
+// A workgroup of WAVES wavefronts owns 32 * WAVES queries of one batch index (32 per wave) and
+// streams the keys in blocks of 32; see the work split below.
 //
 // Orientation: the scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16. In the
 // 32 x 32 accumulator layout lane l then holds one query (column l % 32) and 16 keys (rows
 // 8 g + 4 (l / 32) + j at register 4 g + j), so a row maximum or sum over the keys is a register
 // fold plus one exchange with lane l ^ 32. The Q^T operand (B) is the same for every key block and
-// stays in the scorer's registers. The probabilities P^T are packed to 16 bits and serve as the B
+// stays in registers. The probabilities P^T are packed to 16 bits and serve as the B
 // operand of O^T = V^T P^T: registers 8 s .. 8 s + 7 of a score tile are the B operand of 16-key
 // step s when both operands number the keys of that step in the same permuted order (slot
 // 8 h + 4 r + t holds key 16 s + 8 r + 4 h + t), which the V^T fragment read (ds_read_b64_tr_b16
-// with rows 16 s + 8 r + 4 h + t) follows. P crosses from scorer to accumulator through LDS in
-// exactly this register layout (lane-linear 16-byte stores and loads).
+// with rows 16 s + 8 r + 4 h + t) follows, so P never leaves the registers.
 //
 // Softmax: f32 throughout, online over key blocks in the log2 domain: e = exp2(s * scale * log2 e -
 // m) with v_exp_f32. The subtracted maximum m only moves when the running maximum exceeds it by more
@@ -34,13 +30,14 @@
 // The configuration struct C supplies: DT (0 bf16, 1 f16), HD, WAVES, SQ, SK, NB (batch count), the
 // element strides Q_S, K_S, V_S of one query / key row (the head dimension has stride 1), the batch
 // offset functions q_off(b), k_off(b), v_off(b), CAUSAL and SL (the score scale times log2 e, > 0).
-// O is written row-major as [b][q][128]. The kernel is launched with 128 * WAVES threads.
+// O is written row-major as [b][q][HD]. The kernel is launched with 64 * WAVES threads.
 #pragma once
 
 namespace accy {
 namespace attn {
 
 using gemm::f32x16;
+using gemm::f32x4;
 using gemm::i16x4;
 using gemm::u32x4;
 typedef u32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -71,51 +68,68 @@ constexpr int BK = 32;   // keys per block
 template <int HD> __device__ __forceinline__ int k_swizzle(int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); }
 template <int HD> __device__ __forceinline__ int v_swizzle(int r) { return HD == 128 ? gemm::tr_swizzle(r) : 2 * ((r >> 1) & 1); }
 
-// Issues this wave's share of the K tile of keys [k0, k0 + 32): HD / 16 instructions of 1 KiB.
-template <int WAVES, long KS, int HD>
-__device__ __forceinline__ void load_k(const u16_t* __restrict__ kb, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int PER = HD / 16 / WAVES, LPR = HD / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
+// Byte offsets, within a tile, of one lane's pieces of the K / V tiles, computed once per query
+// block. The per-step accesses then add only compile-time constants (LDS stage, key step) or a scalar
+// base (the key block in global memory), so a step spends no VALU instructions on addresses; the
+// offsets go through an empty asm statement so that the compiler keeps them in registers instead
+// of recomputing them inside the loop.
+template <int HD, int WAVES, long KS, long VS>
+struct TileOffsets {
+  static constexpr int DS = HD / 16, DTN = HD / 32, PER = HD / 16 / WAVES;
+  static constexpr int LPR = HD / 8, RPI = 64 / LPR;  // lanes per 16-byte-chunked row, rows per load
+  u32_t kf[DS];   // K fragment (A operand of S^T) of head-dim step dd: row lane % 32, chunk 2 dd + lane / 32
+  u32_t vf[DTN];  // V^T fragment (ds_read_b64_tr_b16) of head-dim tile dt, for key step 0, half 0
+  u32_t kg[PER];  // this lane's 16-byte chunk of K load i in global memory, and its LDS position
+  u32_t vg[PER];
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+    const int row = lane & 31;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int gi = wave * PER + i;
-    const int row = RPI * gi + lane / LPR;
-    const int c = (lane % LPR) ^ k_swizzle<HD>(row);
-    gemm::dma16(kb + (k0 + row) * KS + 8 * c, (ACCY_LDS void*)(lds + gi * 512));
-  }
-}
-
-template <int WAVES, long VS, int HD>
-__device__ __forceinline__ void load_v(const u16_t* __restrict__ vb, long k0, u16_t* lds, int wave, int lane) {
-  constexpr int PER = HD / 16 / WAVES, LPR = HD / 8, RPI = 64 / LPR;
+    for (int dd = 0; dd < DS; ++dd) kf[dd] = 2u * (u32_t)(row * HD + (((2 * dd + (lane >> 5)) ^ k_swizzle<HD>(row)) << 3));
+    // V^T fragment: lanes 16 g + i read key 4 (g / 2) + i / 4 (+ 16 s + 8 r for key step s, half r, which
+    // the swizzle does not see) at column unit 2 dt + (g & 1), element 4 (i & 3)
+    const int g = lane >> 4, i = lane & 15, k = 4 * (g >> 1) + (i >> 2);
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int gi = wave * PER + i;
-    const int row = RPI * gi + lane / LPR;
-    const int p = lane % LPR;
-    const int u = (p >> 1) ^ v_swizzle<HD>(row);
-    gemm::dma16(vb + (k0 + row) * VS + 16 * u + 8 * (p & 1), (ACCY_LDS void*)(lds + gi * 512));
+    for (int dt = 0; dt < DTN; ++dt) {
+      const int unit = (2 * dt + (g & 1)) ^ v_swizzle<HD>(k);
+      vf[dt] = 2u * (u32_t)(k * HD + unit * 16 + 4 * (i & 3));
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int r = RPI * (wave * PER + j) + lane / LPR, p = lane % LPR;
+      kg[j] = 2u * (u32_t)(r * KS + 8 * ((p ^ k_swizzle<HD>(r))));
+      vg[j] = 2u * (u32_t)(r * VS + 16 * ((p >> 1) ^ v_swizzle<HD>(r)) + 8 * (p & 1));
+    }
+#pragma unroll
+    for (int dd = 0; dd < DS; ++dd) asm volatile("" : "+v"(kf[dd]));
+#pragma unroll
+    for (int dt = 0; dt < DTN; ++dt) asm volatile("" : "+v"(vf[dt]));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) asm volatile("" : "+v"(kg[j]), "+v"(vg[j]));
   }
+};
+
+// Issues one wave's share (PER instructions of 1 KiB) of the tile whose first row starts at element
+// `first` of g, into LDS tile `lds` (16-byte chunk positions as the offsets say).
+template <int PER>
+__device__ __forceinline__ void dma_share(const u16_t* __restrict__ g, long first, const u32_t (&go)[PER], u16_t* lds, int wave) {
+  const char* base = (const char*)(g + first);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) gemm::dma16(base + go[j], (ACCY_LDS void*)(lds + (wave * PER + j) * 512));
 }
 
-// A operand of S^T for the block's 32 keys and head-dim step dd (16 elements).
-template <int HD>
-__device__ __forceinline__ u32x4 k_frag(const u16_t* lds, int dd, int lane) {
-  const int row = lane & 31;
-  const int c = 2 * dd + (lane >> 5);
-  return *(const u32x4*)(lds + row * HD + ((c ^ k_swizzle<HD>(row)) << 3));
-}
+// A operand of S^T for head-dim step dd from K stage `lds`.
+__device__ __forceinline__ u32x4 k_frag(const u16_t* lds, u32_t off) { return *(const u32x4*)((const char*)lds + off); }
 
-// A operand of O^T = V^T P^T for head-dim tile dt (32) and 16-key step s, keys in the permuted order.
+// A operand of O^T = V^T P^T for one head-dim tile (offset off) and 16-key step s, keys in the
+// permuted order: halves r = 0, 1 are rows 16 s + 8 r + ... of the tile.
 template <int HD>
-__device__ __forceinline__ u32x4 v_frag(const u16_t* lds, int dt, int s, int lane) {
-  const int g = lane >> 4, i = lane & 15;
-  const int n0 = dt * 32 + ((g & 1) << 4);
+__device__ __forceinline__ u32x4 v_frag(const u16_t* lds, u32_t off, int s) {
   u32x4 out;
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const int k = 16 * s + 8 * r + 4 * (g >> 1) + (i >> 2);
-    const int unit = (n0 >> 4) ^ v_swizzle<HD>(k);
-    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((ACCY_LDS i16x4*)(lds + k * HD + unit * 16 + 4 * (i & 3)));
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (ACCY_LDS i16x4*)((const char*)lds + off + 2 * (16 * s + 8 * r) * HD));
     out[2 * r] = (u32_t)(u16_t)v[0] | ((u32_t)(u16_t)v[1] << 16);
     out[2 * r + 1] = (u32_t)(u16_t)v[2] | ((u32_t)(u16_t)v[3] << 16);
   }
@@ -178,9 +192,10 @@ __device__ __forceinline__ void with_partner(float x, float& r0, float& r1) {
   r1 = __builtin_bit_cast(float, b);
 }
 __device__ __forceinline__ float max_with_partner(float x) {
-  float a, b;
+  float a, b, r;
   with_partner(x, a, b);
-  return fmaxf(a, b);
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));  // no canonicalising moves (no signalling NaNs here)
+  return r;
 }
 __device__ __forceinline__ float sum_with_partner(float x) {
   float a, b;
@@ -188,324 +203,267 @@ __device__ __forceinline__ float sum_with_partner(float x) {
   return a + b;
 }
 
-// Work split. Each group of 64 queries is served by two waves, which the hardware places on one
-// SIMD (waves w and w + WAVES of a workgroup of 2 * WAVES waves):
-//  * the scorer computes S = K Q^T and the softmax and writes P (16-bit, already in the MFMA
-//    B-operand layout) and the rescale factors to LDS;
-//  * the accumulator reads them back and runs O^T += V^T P^T, then normalises and stores O.
-// Each wave then fits in half the register file (the scorer holds Q^T and two score sets, the
-// accumulator O), so the two share a SIMD, and the scorer's softmax VALU work issues while the
-// accumulator's MFMAs run. Step t of the workgroup (one barrier each, nkb + 2 steps):
-//  * scorer: S(t) for t < nkb, with the softmax of block t - 1 slotted between its 16 MFMAs (slots
-//    0-3 row maxima, slot 4 the exchange with the partner lane and the rare rescale, slots 5-15
-//    exp2, partial sums and packing); P(t - 1) and the factors go to buffer (t - 1) % 2;
-//  * accumulator: for t >= 2, block t - 2 from buffer t % 2 and V stage (t - 2) % 4.
-// K tiles are loaded by the scorers two steps ahead (K(t + 2) at step t), V tiles by the
-// accumulators two steps before use (V(t) at step t); both have four LDS stages. A P buffer written
-// at step t is read at step t + 1 and rewritten at step t + 2, after the barrier that follows the
-// reads.
+// Work split. Every wave owns 32 queries and does all of their work: S^T = K Q^T, the online
+// softmax and O^T += V^T P^T, with P kept in registers (the score registers of a block, packed in
+// pairs, are the B operand of its P.V product as they stand). Two waves share each SIMD (one
+// workgroup of eight waves per CU, or two of four): each wave interleaves its own MFMAs with its
+// softmax VALU work, and the two waves take turns on the matrix core.
+// Step t of a query block (one workgroup barrier each, nkb + 2 steps), on K stage t % 4:
+//  * the MFMAs of S(t) (HD / 16, for t < nkb) alternate with those of P(t - 2).V(t - 2) (HD / 16,
+//    for t >= 2, V stage (t - 2) % 4);
+//  * the softmax of block t - 1 (for 1 <= t <= nkb) runs in 13 slots between them: slots 0-3 the
+//    row maximum, slot 4 the exchange with the partner lane and the decision whether the
+//    subtracted maximum moves, slots 5-12 exp2, packing and the row sum of one pair of scores each;
+//  * at the end of the step O is rescaled for block t - 1 when its maximum moved (rarely), between
+//    the P.V of block t - 2 and that of block t - 1;
+//  * K(t + 2) and V(t) are issued to their stages after the barrier, so both are two steps ahead
+//    of their use and every stage is rewritten only after the barrier that follows its last read.
+// What bounds it (C4 on MI355X): the chip's power limit. The MFMAs, the softmax's ~90 VALU
+// instructions per wave and step and the LDS reads add up to about the measured time, and the
+// clock drops as the work per cycle rises; every instruction removed from the loop counts.
 template <class C>
 struct Lds {
-  static constexpr int WAVES = C::WAVES;
   u16_t* const* ks;  // K stages [4][BK * HD]
   u16_t* const* vs;  // V stages [4][BK * HD]
-  u32x4* pb;         // P: [2][WAVES][QT * 2][64] u32x4
-  float* ab;         // rescale factors: [2][WAVES][64][QT]
-  float* lb;         // row sums for the epilogue: [WAVES][64][QT]
 };
 
 template <class C>
-struct Scorer {
-  static constexpr int HD = C::HD, WAVES = C::WAVES, QT = 2, DS = HD / 16;
-  static constexpr int NS = QT * DS;            // score MFMAs per key block (16 for HD 128, 8 for HD 64)
-  static constexpr int PER = HD / 16 / WAVES;  // K load instructions per wave per key block
-  static constexpr long NQB = C::SQ / (64 * WAVES), NKB = C::SK / BK;
+struct Worker {
+  static constexpr int HD = C::HD, WAVES = C::WAVES, DS = HD / 16, DTN = HD / 32;
+  static constexpr int NPV = 2 * DTN;          // P.V MFMAs per key block (= DS score MFMAs)
+  static constexpr int PER = HD / 16 / WAVES;  // K and V load instructions per wave per key block
+  static_assert(NPV == DS, "score and P.V MFMAs alternate one for one");
 
   Lds<C> sh;
   const u16_t* __restrict__ kb;
-  u32x4 qf[QT][DS];
-  f32x16 s[2][QT];  // scores of the blocks of even / odd index
-  float m[QT], l[QT];
+  const u16_t* __restrict__ vb;
+  TileOffsets<HD, WAVES, C::K_S, C::V_S> off;
+  u32x4 qf[DS];    // Q^T, the B operand of S^T for head-dim step dd
+  f32x16 s[2];     // scores of the blocks of even / odd index
+  f32x16 o[DTN];   // O^T, head-dim tile dt
+  u32x4 p[2][2];   // P of the blocks of even / odd index: the B operands of their two 16-key steps
+  float alpha[2];  // factor for O and l of the block of even / odd index (1 if the maximum did not move)
+  float m, l;      // subtracted maximum (log2 domain, finite) and this lane's half of the row sum
   long q0;
   int wave, lane;
 
-  __device__ __forceinline__ long query(int qt) const { return q0 + 32 * (qt * WAVES + wave) + (lane & 31); }
+  __device__ __forceinline__ long query() const { return q0 + 32 * wave + (lane & 31); }
 
-  // Scores of keys above the query are -inf (blocks that cross the diagonal only).
+  // Scores of keys above the query are -inf (blocks that cross the diagonal only). Register r holds
+  // key k0 + 8 (r / 4) + 4 (lane / 32) + r % 4, so the test is one 32-bit compare of a constant
+  // against the lane's threshold (query - k0 - 4 (lane / 32)).
   template <int PB>
   __device__ __forceinline__ void mask(long k0) {
-    if (k0 + BK - 1 <= q0) return;
+    if (k0 + BK - 1 <= q0 + 32 * wave) return;
+    const int th = (int)(query() - k0) - 4 * (lane >> 5);
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      const long qi = query(qt);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const long ki = k0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (ki > qi) s[PB][qt][r] = -__builtin_inff();
-      }
-    }
+    for (int r = 0; r < 16; ++r)
+      if (8 * (r >> 2) + (r & 3) > th) s[PB][r] = -__builtin_inff();
   }
 
-  // Softmax work of slot T on the scores in set PB; p receives P as MFMA B operands, alpha the
-  // factor by which the accumulated O is to be scaled before P.V of this block (1 if unchanged).
+  // Softmax, first part, for the block in score set PB, as slots 0-4 between the MFMAs: the row
+  // maximum in two max3 chains (slots 0-3), then (slot 4) the partner lane's half, the decision whether
+  // the subtracted maximum m moves (only when the new one exceeds it by more than 8) and the factor
+  // alpha for O and l. m starts at -FLT_MAX rather than -inf, so that s * SL - m is -inf exactly for
+  // the masked scores and no select is needed.
   template <int PB, int T>
-  __device__ __forceinline__ void softmax_slot(float (&mx)[QT], float (&msub)[QT], float (&ls)[QT][4], u32x4 (&p)[QT][2],
-                                               float (&alpha)[QT]) {
-    f32x16 (&sp)[QT] = s[PB];
-    if constexpr (T < 4) {
-      constexpr int qt = T >> 1, r0 = 8 * (T & 1);
-#pragma unroll
-      for (int r = 0; r < 8; r += 2) mx[qt] = max3(mx[qt], sp[qt][r0 + r], sp[qt][r0 + r + 1]);
-    } else if constexpr (T == 4) {
-      bool need[QT];
-      float mn[QT];
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        mn[qt] = max_with_partner(mx[qt]) * C::SL;
-        need[qt] = mn[qt] > m[qt] + 8.0f;
-        alpha[qt] = 1.0f;
-      }
-      if (__any(need[0] || need[1])) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-          alpha[qt] = need[qt] ? __builtin_amdgcn_exp2f(m[qt] - mn[qt]) : 1.0f;
-          m[qt] = need[qt] ? mn[qt] : m[qt];
-          l[qt] *= alpha[qt];
-        }
-      }
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) msub[qt] = m[qt] == -__builtin_inff() ? 0.0f : m[qt];
+  __device__ __forceinline__ void max_slot(float& ma, float& mb) {
+    const f32x16& sp = s[PB];
+    if constexpr (T == 0) {
+      ma = max3(sp[0], sp[1], sp[2]);
+      mb = max3(sp[3], sp[4], sp[5]);
+    } else if constexpr (T < 4) {
+      ma = max3(ma, sp[2 + 4 * T], sp[3 + 4 * T]);
+      mb = max3(mb, sp[4 + 4 * T], sp[5 + 4 * T]);
     } else {
-      // 32 elements over slots 5..15; element e: qt = e / 16, r = e % 16.
-      For<(T - 5) * 32 / 11, (T - 4) * 32 / 11>::run([&](auto ei) {
-        constexpr int e = decltype(ei)::value, qt = e >> 4, r = e & 15;
-        const float x = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[qt][r], C::SL, -msub[qt]));
-        sp[qt][r] = x;
-        if constexpr (r & 1) {
-          const u32_t pair = pack2<C::DT>(sp[qt][r - 1], x);
-          p[qt][r >> 3][(r & 7) >> 1] = pair;
-          ls[qt][(r >> 1) & 3] = add_pair<C::DT>(pair, ls[qt][(r >> 1) & 3]);
-        }
-      });
+      // T == 4: scores 14 and 15, then the exchange and the decision
+      const float mn = max_with_partner(max3(ma, mb, max3(sp[14], sp[15], sp[15]))) * C::SL;
+      const bool need = mn > m + 8.0f;
+      // branch-free, so that the step body stays one scheduling region
+      const float a = __builtin_amdgcn_exp2f(m - mn);
+      alpha[PB] = need ? a : 1.0f;
+      m = need ? mn : m;
+      l *= alpha[PB];
     }
   }
 
-  // Scores of one block into set SB from K stage ST, with the softmax of set PB when PREV.
-  template <int ST, int SB, int PB, bool PREV>
-  __device__ __forceinline__ void scores(long kprev0, u32x4 (&p)[QT][2], float (&alpha)[QT]) {
+  // Softmax, second part, for scores 2 j and 2 j + 1 of the block in set PB: P = exp2(s * SL - m),
+  // packed to 16 bits (the B operand of 16-key step j / 4), and the packed pair's exact sum into l.
+  template <int PB, int J>
+  __device__ __forceinline__ void pair(float ml) {
+    f32x16& sp = s[PB];
+    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[2 * J], C::SL, ml));
+    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[2 * J + 1], C::SL, ml));
+    const u32_t pr = pack2<C::DT>(e0, e1);
+    p[PB][J >> 2][J & 3] = pr;
+    l = add_pair<C::DT>(pr, l);
+  }
+
+  // Step t on K stage ST = t % 4: S(t) when HS, the softmax of block t - 1 when HM, P.V of block
+  // t - 2 when HP. Score sets, P sets and factors of block j live at index j % 2.
+  template <int ST, bool HS, bool HM, bool HP>
+  __device__ __forceinline__ void step(long t, long nkb) {
+    constexpr int SB = ST & 1, PB = SB ^ 1, NE = (HS ? DS : 0) + (HP ? NPV : 0);
+    constexpr int VST = (ST + 2) & 3;
+    // K(t) and V(t - 2) were issued at step t - 2; K(t + 1) and V(t - 1) at step t - 1 may still fly.
+    if (t + 1 < nkb) gemm::wait_vmcnt<2 * PER>();
+    else if (t - 1 < nkb) gemm::wait_vmcnt<PER>();
+    else gemm::wait_vmcnt<0>();
+    gemm::lds_reads_done_barrier();
+    if (t + 2 < nkb) dma_share<PER>(kb, (t + 2) * BK * C::K_S, off.kg, sh.ks[(ST + 2) & 3], wave);
+    if (t < nkb) dma_share<PER>(vb, t * BK * C::V_S, off.vg, sh.vs[ST], wave);
+    if constexpr (HM)
+      if constexpr (C::CAUSAL) mask<PB>((t - 1) * BK);
+
     const u16_t* kl = sh.ks[ST];
-    float mx[QT], msub[QT], ls[QT][4];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      mx[qt] = -__builtin_inff();
-      msub[qt] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ls[qt][i] = 0.0f;
-      s[SB][qt] = f32x16{};
+    const u16_t* vl = sh.vs[VST];
+    constexpr int PF = 2;  // fragments read ahead of their MFMA
+    u32x4 kf[PF + 1], vf[PF + 1];
+    if constexpr (HS) {
+      For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < DS) kf[i] = k_frag(kl, off.kf[i]); });
+      s[SB] = f32x16{};
     }
-    if constexpr (PREV && C::CAUSAL) mask<PB>(kprev0);
-    u32x4 a = k_frag<HD>(kl, 0, lane), an = a;
-    For<0, NS>::run([&](auto ti) {
-      constexpr int t = decltype(ti)::value, dd = t >> 1, qt = t & 1;
-      if constexpr (qt == 0 && t + 2 < NS) an = k_frag<HD>(kl, (t + 2) >> 1, lane);
-      s[SB][qt] = gemm::mfma32x32x16<C::DT>(a, qf[qt][dd], s[SB][qt]);
-      if constexpr (qt == 1) a = an;
+    if constexpr (HP)
+      For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < NPV) vf[i] = v_frag<HD>(vl, off.vf[i / 2], i % 2); });
+    // The softmax of block t - 1 as 13 slots: max slots 0-4, then pairs 0-7 (slot 5 + j). Slot 0 runs
+    // while the first fragments arrive, the others between the MFMAs.
+    float ma, mb, ml = 0.0f;
+    auto slot = [&](auto ci) {
+      constexpr int c = decltype(ci)::value;
+      if constexpr (c < 5) {
+        max_slot<PB, c>(ma, mb);
+        if constexpr (c == 4) ml = -m;
+      } else {
+        pair<PB, c - 5>(ml);
+      }
+    };
+    if constexpr (HM) slot(Int<0>{});
+    __builtin_amdgcn_sched_barrier(0);
+    For<0, NE>::run([&](auto ei) {
+      constexpr int e = decltype(ei)::value;
+      // event e: score MFMA e / 2 and P.V MFMA e / 2 alternate when both are present
+      constexpr bool is_s = HS && (!HP || (e & 1) == 0);
+      constexpr int i = HS && HP ? e / 2 : e;
+      if constexpr (is_s) {
+        if constexpr (i + PF < DS) kf[(i + PF) % (PF + 1)] = k_frag(kl, off.kf[i + PF]);
+        s[SB] = gemm::mfma32x32x16<C::DT>(kf[i % (PF + 1)], qf[i], s[SB]);
+      } else {
+        // P.V MFMA i: head-dim tile i / 2, 16-key step i % 2
+        if constexpr (i + PF < NPV) vf[(i + PF) % (PF + 1)] = v_frag<HD>(vl, off.vf[(i + PF) / 2], (i + PF) % 2);
+        o[i / 2] = gemm::mfma32x32x16<C::DT>(vf[i % (PF + 1)], p[SB][i % 2], o[i / 2]);
+      }
       __builtin_amdgcn_sched_barrier(0);
-      // the 16 softmax slots of the previous block, spread over this block's NS MFMAs
-      if constexpr (PREV)
-        For<t * 16 / NS, (t + 1) * 16 / NS>::run([&](auto si) { softmax_slot<PB, decltype(si)::value>(mx, msub, ls, p, alpha); });
+      if constexpr (HM) For<1 + e * 12 / NE, 1 + (e + 1) * 12 / NE>::run(slot);
       __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (PREV) {
+    if constexpr (HM) {
+      if constexpr (NE == 0) For<1, 13>::run(slot);
+      // The softmax results are consumed here, so that no pass sinks their VALU work past the next
+      // barrier (out of the MFMA slots it was placed in).
+      asm volatile("" : "+v"(p[PB][0]), "+v"(p[PB][1]), "+v"(l), "+v"(alpha[PB]));
+      // O is rescaled for block t - 1 after this step's P.V of block t - 2 and before the next step's
+      // P.V of block t - 1 (rarely: only when the maximum moved).
+      if (__any(alpha[PB] != 1.0f)) {
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) l[qt] += (ls[qt][0] + ls[qt][1]) + (ls[qt][2] + ls[qt][3]);
+        for (int dt = 0; dt < DTN; ++dt) o[dt] *= alpha[PB];
+      }
     }
   }
 
-  // Softmax of the last block (set PB), with no scores to overlap with.
-  template <int PB>
-  __device__ __forceinline__ void softmax_only(long k0, u32x4 (&p)[QT][2], float (&alpha)[QT]) {
-    if constexpr (C::CAUSAL) mask<PB>(k0);
-    float mx[QT], msub[QT], ls[QT][4];
+  // One query block: prologue (Q^T into registers, K(0) and K(1) issued), nkb + 2 steps, epilogue.
+  __device__ __forceinline__ void run(const u16_t* __restrict__ qp, u16_t* __restrict__ out, long b, long nkb) {
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      mx[qt] = -__builtin_inff();
-      msub[qt] = 0.0f;
+    for (int dd = 0; dd < DS; ++dd) qf[dd] = *(const u32x4*)(qp + query() * C::Q_S + 16 * dd + 8 * (lane >> 5));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) ls[qt][i] = 0.0f;
-    }
-    For<0, 16>::run([&](auto ti) { softmax_slot<PB, decltype(ti)::value>(mx, msub, ls, p, alpha); });
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) l[qt] += (ls[qt][0] + ls[qt][1]) + (ls[qt][2] + ls[qt][3]);
-  }
-
-  // P and the rescale factors of one block into buffer PBUF (lane-linear, conflict-free).
-  template <int PBUF>
-  __device__ __forceinline__ void publish(const u32x4 (&p)[QT][2], const float (&alpha)[QT]) {
-    u32x4* pw = sh.pb + (PBUF * WAVES + wave) * (QT * 2 * 64) + lane;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) pw[(qt * 2 + st) * 64] = p[qt][st];
-    float* aw = sh.ab + ((PBUF * WAVES + wave) * 64 + lane) * QT;
-    *(f32x2*)aw = f32x2{alpha[0], alpha[1]};
-  }
-
-  // Step t (1 <= t < nkb) on K stage ST = t % 4.
-  template <int ST>
-  __device__ __forceinline__ void step(long t, long nkb) {
-    if (t + 1 < nkb) gemm::wait_vmcnt<PER>();
-    else gemm::wait_vmcnt<0>();
-    gemm::lds_reads_done_barrier();
-    if (t + 2 < nkb) load_k<WAVES, C::K_S, HD>(kb, (t + 2) * BK, sh.ks[(ST + 2) & 3], wave, lane);
-    u32x4 p[QT][2];
-    float alpha[QT];
-    scores<ST, ST & 1, (ST + 1) & 1, true>((t - 1) * BK, p, alpha);
-    publish<(ST + 1) & 1>(p, alpha);
-  }
-
-  // Step nkb: the softmax of the last block (index nkb - 1, score set and buffer PB).
-  template <int PB>
-  __device__ __forceinline__ void last_step(long nkb) {
-    gemm::lds_reads_done_barrier();
-    u32x4 p[QT][2];
-    float alpha[QT];
-    softmax_only<PB>((nkb - 1) * BK, p, alpha);
-    publish<PB>(p, alpha);
-  }
-
-  __device__ __forceinline__ void run(const u16_t* __restrict__ qp, long nkb) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int dd = 0; dd < DS; ++dd) qf[qt][dd] = *(const u32x4*)(qp + query(qt) * C::Q_S + 16 * dd + 8 * (lane >> 5));
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      m[qt] = -__builtin_inff();
-      l[qt] = 0.0f;
-    }
-    load_k<WAVES, C::K_S, HD>(kb, 0, sh.ks[0], wave, lane);
-    if (nkb > 1) load_k<WAVES, C::K_S, HD>(kb, BK, sh.ks[1], wave, lane);
-    // Step 0: scores of block 0 only.
+    for (int dt = 0; dt < DTN; ++dt) o[dt] = f32x16{};
+    m = -0x1.fffffep127f;
+    l = 0.0f;
+    alpha[0] = alpha[1] = 1.0f;
+    off.init(wave, lane);
+    dma_share<PER>(kb, 0, off.kg, sh.ks[0], wave);
+    if (nkb > 1) dma_share<PER>(kb, BK * C::K_S, off.kg, sh.ks[1], wave);
+    // Step 0 waits for K(0) only (K(1) may fly); the general rule below counts K(1) as issued at
+    // step -1.
     if (nkb > 1) gemm::wait_vmcnt<PER>();
     else gemm::wait_vmcnt<0>();
-    gemm::lds_reads_done_barrier();
-    if (nkb > 2) load_k<WAVES, C::K_S, HD>(kb, 2 * BK, sh.ks[2], wave, lane);
-    {
-      u32x4 unused_p[QT][2];
-      float unused_a[QT];
-      scores<0, 0, 1, false>(0, unused_p, unused_a);
+    step0(nkb);
+    if (nkb == 1) {
+      step<1, false, true, false>(1, nkb);
+      step<2, false, false, true>(2, nkb);
+    } else {
+      steps(nkb);
     }
-    long t = 1;
-    for (; t + 3 < nkb; t += 4) {
-      step<1>(t, nkb);
-      step<2>(t + 1, nkb);
-      step<3>(t + 2, nkb);
-      step<0>(t + 3, nkb);
-    }
-    if (t < nkb) step<1>(t, nkb);
-    if (t + 1 < nkb) step<2>(t + 1, nkb);
-    if (t + 2 < nkb) step<3>(t + 2, nkb);
-    if ((nkb - 1) & 1) last_step<1>(nkb);
-    else last_step<0>(nkb);
-    // Row sums (both lanes of a query) for the accumulator's epilogue, then step nkb + 1.
-    float* lw = sh.lb + (wave * 64 + lane) * QT;
-    *(f32x2*)lw = f32x2{sum_with_partner(l[0]), sum_with_partner(l[1])};
-    gemm::lds_reads_done_barrier();
+    epilogue(out, b);
   }
-};
 
-template <class C>
-struct Accumulator {
-  static constexpr int HD = C::HD, WAVES = C::WAVES, QT = 2, DTN = HD / 32;
-  static constexpr int NA = DTN * 2 * QT;      // P.V MFMAs per key block (16 for HD 128, 8 for HD 64)
-  static constexpr int PER = HD / 16 / WAVES;  // V load instructions per wave per key block
+  // Steps 1 .. nkb + 1 for nkb >= 2. The steady-state loop leaves t = 2 (mod 4), so the stage of
+  // every remaining step is known; r = nkb - t scored steps remain (0 .. 3).
+  __device__ __forceinline__ void steps(long nkb) {
+    step<1, true, true, false>(1, nkb);
+    long t = 2;
+    for (; t + 3 < nkb; t += 4) {
+      step<2, true, true, true>(t, nkb);
+      step<3, true, true, true>(t + 1, nkb);
+      step<0, true, true, true>(t + 2, nkb);
+      step<1, true, true, true>(t + 3, nkb);
+    }
+    // nkb % 4 is known at compile time in the common shapes (non-causal, or causal with query blocks
+    // and key counts that are multiples of 128); then only that tail is compiled.
+    constexpr long BQ = 32 * WAVES, NKB = C::SK / BK;
+    constexpr int MOD = !C::CAUSAL ? (int)((NKB - 2) % 4) : (BQ % 128 == 0 && C::SK % 128 == 0 ? 2 : -1);
+    const long r = MOD >= 0 ? MOD : nkb - t;
+    if (r == 0) {
+      step<2, false, true, true>(t, nkb);
+      step<3, false, false, true>(t + 1, nkb);
+    } else if (r == 1) {
+      step<2, true, true, true>(t, nkb);
+      step<3, false, true, true>(t + 1, nkb);
+      step<0, false, false, true>(t + 2, nkb);
+    } else if (r == 2) {
+      step<2, true, true, true>(t, nkb);
+      step<3, true, true, true>(t + 1, nkb);
+      step<0, false, true, true>(t + 2, nkb);
+      step<1, false, false, true>(t + 3, nkb);
+    } else {
+      step<2, true, true, true>(t, nkb);
+      step<3, true, true, true>(t + 1, nkb);
+      step<0, true, true, true>(t + 2, nkb);
+      step<1, false, true, true>(t + 3, nkb);
+      step<2, false, false, true>(t + 4, nkb);
+    }
+  }
 
-  Lds<C> sh;
-  const u16_t* __restrict__ vb;
-  f32x16 o[QT][DTN];
-  long q0;
-  int wave, lane;
-
-  __device__ __forceinline__ long query(int qt) const { return q0 + 32 * (qt * WAVES + wave) + (lane & 31); }
-
-  // O^T = alpha O^T + V^T P^T for the block in P buffer PBUF and V stage VST.
-  template <int PBUF, int VST>
-  __device__ __forceinline__ void consume() {
-    const u32x4* pr = sh.pb + (PBUF * WAVES + wave) * (QT * 2 * 64) + lane;
-    const f32x2 al = *(const f32x2*)(sh.ab + ((PBUF * WAVES + wave) * 64 + lane) * QT);
-    u32x4 p[QT][2];
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int st = 0; st < 2; ++st) p[qt][st] = pr[(qt * 2 + st) * 64];
-    const u16_t* vl = sh.vs[VST];
-    u32x4 vf[DTN][2];
+  // O = O^T / l, rounded to the element type, row-major [b][q][HD].
+  __device__ __forceinline__ void epilogue(u16_t* __restrict__ out, long b) {
+    const float inv = 1.0f / sum_with_partner(l);
+    const int h = lane >> 5;
+    u16_t* __restrict__ orow = out + (b * C::SQ + query()) * HD;
 #pragma unroll
     for (int dt = 0; dt < DTN; ++dt)
 #pragma unroll
-      for (int st = 0; st < 2; ++st) vf[dt][st] = v_frag<HD>(vl, dt, st, lane);
-    if (__any(al.x != 1.0f || al.y != 1.0f)) {
-#pragma unroll
-      for (int dt = 0; dt < DTN; ++dt) {
-        o[0][dt] *= al.x;
-        o[1][dt] *= al.y;
+      for (int g = 0; g < 4; ++g) {
+        const f32x16& acc = o[dt];
+        const u32_t lo = pack2_out<C::DT>(acc[4 * g] * inv, acc[4 * g + 1] * inv);
+        const u32_t hi = pack2_out<C::DT>(acc[4 * g + 2] * inv, acc[4 * g + 3] * inv);
+        *(u32x2*)(orow + dt * 32 + 8 * g + 4 * h) = u32x2{lo, hi};
       }
-    }
-    For<0, NA>::run([&](auto ti) {
-      constexpr int t = decltype(ti)::value, dt = t >> 2, st = (t >> 1) & 1, qt = t & 1;
-      o[qt][dt] = gemm::mfma32x32x16<C::DT>(vf[dt][st], p[qt][st], o[qt][dt]);
+  }
+
+  // Step 0: barrier, K(2) and V(0) issued, S(0).
+  __device__ __forceinline__ void step0(long nkb) {
+    gemm::lds_reads_done_barrier();
+    if (2 < nkb) dma_share<PER>(kb, 2 * BK * C::K_S, off.kg, sh.ks[2], wave);
+    dma_share<PER>(vb, 0, off.vg, sh.vs[0], wave);
+    const u16_t* kl = sh.ks[0];
+    u32x4 kf[3];
+    kf[0] = k_frag(kl, off.kf[0]);
+    kf[1] = k_frag(kl, off.kf[1]);
+    s[0] = f32x16{};
+    For<0, DS>::run([&](auto ii) {
+      constexpr int i = decltype(ii)::value;
+      if constexpr (i + 2 < DS) kf[(i + 2) % 3] = k_frag(kl, off.kf[i + 2]);
+      s[0] = gemm::mfma32x32x16<C::DT>(kf[i % 3], qf[i], s[0]);
     });
-  }
-
-  // Step t >= 2 on stage ST = t % 4: V(t) is issued, block t - 2 consumed.
-  template <int ST>
-  __device__ __forceinline__ void step(long t, long nkb) {
-    if (t - 1 < nkb) gemm::wait_vmcnt<PER>();
-    else gemm::wait_vmcnt<0>();
-    gemm::lds_reads_done_barrier();
-    if (t < nkb) load_v<WAVES, C::V_S, HD>(vb, t * BK, sh.vs[ST], wave, lane);
-    consume<ST & 1, (ST + 2) & 3>();
-  }
-
-  __device__ __forceinline__ void run(u16_t* __restrict__ out, long b, long nkb) {
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-      for (int dt = 0; dt < DTN; ++dt) o[qt][dt] = f32x16{};
-    // Steps 0 and 1: V(0) and V(1) are issued.
-    gemm::lds_reads_done_barrier();
-    load_v<WAVES, C::V_S, HD>(vb, 0, sh.vs[0], wave, lane);
-    gemm::lds_reads_done_barrier();
-    if (nkb > 1) load_v<WAVES, C::V_S, HD>(vb, BK, sh.vs[1], wave, lane);
-    // Steps 2 .. nkb + 1.
-    long t = 2;
-    for (; t + 3 <= nkb + 1; t += 4) {
-      step<2>(t, nkb);
-      step<3>(t + 1, nkb);
-      step<0>(t + 2, nkb);
-      step<1>(t + 3, nkb);
-    }
-    if (t <= nkb + 1) step<2>(t, nkb);
-    if (t + 1 <= nkb + 1) step<3>(t + 1, nkb);
-    if (t + 2 <= nkb + 1) step<0>(t + 2, nkb);
-
-    const f32x2 lsum = *(const f32x2*)(sh.lb + (wave * 64 + lane) * QT);
-    const float inv[QT] = {1.0f / lsum.x, 1.0f / lsum.y};
-    const int h = lane >> 5;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      u16_t* __restrict__ orow = out + (b * C::SQ + query(qt)) * HD;
-#pragma unroll
-      for (int dt = 0; dt < DTN; ++dt)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x16& acc = o[qt][dt];
-          const u32_t lo = pack2_out<C::DT>(acc[4 * g] * inv[qt], acc[4 * g + 1] * inv[qt]);
-          const u32_t hi = pack2_out<C::DT>(acc[4 * g + 2] * inv[qt], acc[4 * g + 3] * inv[qt]);
-          *(u32x2*)(orow + dt * 32 + 8 * g + 4 * h) = u32x2{lo, hi};
-        }
-    }
   }
 };
 
@@ -514,62 +472,46 @@ struct Accumulator {
 // blocks (the heavy blocks start first); the grid is NB * NQB / blocks_per_group workgroups.
 template <class C>
 constexpr long blocks_per_group() {
-  constexpr long NQB = C::SQ / (64 * C::WAVES);
+  constexpr long NQB = C::SQ / (32 * C::WAVES);
   return C::CAUSAL && NQB % 2 == 0 ? 2 : 1;
 }
 
-// One query block (queries qb * 64 * WAVES ...) of batch index b, by the workgroup's scorer and
-// accumulator waves. Both roles meet nkb + 2 barriers, so blocks can follow each other.
+// One query block (queries qb * 32 * WAVES ...) of batch index b. Every wave meets nkb + 2
+// barriers, so blocks can follow each other.
 template <class C>
 __device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
                                             const u16_t* __restrict__ V, u16_t* __restrict__ O, long b, long qb) {
-  constexpr int WAVES = C::WAVES;
-  constexpr long BQ = 64 * WAVES, NKB = C::SK / BK;
+  constexpr long BQ = 32 * C::WAVES, NKB = C::SK / BK;
   const long q0 = qb * BQ;
   long nkb = NKB;
   if constexpr (C::CAUSAL) {
     const long last = (q0 + BQ - 1) / BK + 1;
     nkb = last < nkb ? last : nkb;
   }
-  // The wave index is uniform across the wave; readfirstlane lets the compiler branch on the role.
-  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int lane = (int)(threadIdx.x & 63);
-  if (w < WAVES) {
-    Scorer<C> f;
-    f.sh = sh;
-    f.kb = K + C::k_off(b);
-    f.q0 = q0;
-    f.wave = w;
-    f.lane = lane;
-    f.run(Q + C::q_off(b), nkb);
-  } else {
-    Accumulator<C> f;
-    f.sh = sh;
-    f.vb = V + C::v_off(b);
-    f.q0 = q0;
-    f.wave = w - WAVES;
-    f.lane = lane;
-    f.run(O, b, nkb);
-  }
+  Worker<C> f;
+  f.sh = sh;
+  f.kb = K + C::k_off(b);
+  f.vb = V + C::v_off(b);
+  f.q0 = q0;
+  f.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  f.lane = (int)(threadIdx.x & 63);
+  f.run(Q + C::q_off(b), O, b, nkb);
 }
 
-// Workgroup of 2 * C::WAVES waves (128 * C::WAVES threads) over blocks_per_group<C>() query blocks
-// of 64 * C::WAVES queries of one batch index.
+// Workgroup of C::WAVES waves (64 * C::WAVES threads) over blocks_per_group<C>() query blocks of
+// 32 * C::WAVES queries of one batch index.
 template <class C>
 __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
                                       const u16_t* __restrict__ V, u16_t* __restrict__ O) {
-  constexpr int WAVES = C::WAVES, QT = 2, HD = C::HD;
-  constexpr long BQ = 64 * WAVES, NQB = C::SQ / BQ, PAIR = blocks_per_group<C>(), PER_B = NQB / PAIR;
+  constexpr int WAVES = C::WAVES, HD = C::HD;
+  constexpr long BQ = 32 * WAVES, NQB = C::SQ / BQ, PAIR = blocks_per_group<C>(), PER_B = NQB / PAIR;
   static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
-  static_assert((HD == 64 || HD == 128) && (HD / 16) % WAVES == 0, "head dimension 64 or 128");
+  static_assert((HD == 64 || HD == 128) && (HD / 16) % WAVES == 0, "head dimension 64 or 128, whole load shares");
   __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
   __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
-  __shared__ __attribute__((aligned(16))) u32x4 pbuf[2 * WAVES * QT * 2 * 64];
-  __shared__ __attribute__((aligned(16))) float abuf[2 * WAVES * 64 * QT];
-  __shared__ __attribute__((aligned(16))) float lbuf[WAVES * 64 * QT];
   u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
   u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
-  const Lds<C> sh{ks, vs, pbuf, abuf, lbuf};
+  const Lds<C> sh{ks, vs};
 
   // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
   // query blocks with the most keys start first.
@@ -579,9 +521,12 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   const long b = t / PER_B, p = t % PER_B;
   if (b >= C::NB) return;  // a grid larger than the work
   if constexpr (PAIR == 2) {
-    flash_block<C>(sh, Q, K, V, O, b, NQB - 1 - p);
-    gemm::wait_vmcnt<0>();  // the first block's output stores, before the second block's waits
-    flash_block<C>(sh, Q, K, V, O, b, p);
+    // one copy of the block code, run twice
+#pragma unroll 1
+    for (int i = 0; i < 2; ++i) {
+      flash_block<C>(sh, Q, K, V, O, b, i == 0 ? NQB - 1 - p : p);
+      gemm::wait_vmcnt<0>();  // the block's output stores, before the next block's waits
+    }
   } else {
     flash_block<C>(sh, Q, K, V, O, b, C::CAUSAL ? NQB - 1 - p : p);
   }

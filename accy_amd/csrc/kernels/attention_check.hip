@@ -6,7 +6,7 @@
 #include "attention.h"
 
 struct CheckAttnF16 {
-  static constexpr int DT = 1, HD = 128, WAVES = 4;
+  static constexpr int DT = 1, HD = 128, WAVES = 8;
   static constexpr long SQ = 4096, SK = 4096, NB = 32;
   static constexpr long Q_S = 128, K_S = 128, V_S = 128;
   static constexpr bool CAUSAL = false;
@@ -38,7 +38,7 @@ struct CheckAttnHd64Bf16 {
   static __device__ __forceinline__ long v_off(long b) { return b * 65536L; }
 };
 
-extern "C" __global__ void __launch_bounds__(512) accy_check_attention_hd64_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
+extern "C" __global__ void __launch_bounds__(256) accy_check_attention_hd64_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
   accy::attn::flash<CheckAttnHd64Bf16>(q, k, v, o);
 }
 
@@ -46,7 +46,7 @@ extern "C" __global__ void __launch_bounds__(512) accy_check_attention_f16(const
   accy::attn::flash<CheckAttnF16>(q, k, v, o);
 }
 
-extern "C" __global__ void __launch_bounds__(512) accy_check_attention_causal_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
+extern "C" __global__ void __launch_bounds__(256) accy_check_attention_causal_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
   accy::attn::flash<CheckAttnCausalBf16>(q, k, v, o);
 }
 

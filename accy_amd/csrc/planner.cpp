@@ -1592,8 +1592,8 @@ class Planner {
     if (L.q.strides[qc] != 1 || L.k.strides[kc] != 1 || L.v.strides[(size_t)vf] != 1) return false;
     L.sq = qt.dims[(size_t)qf].extent;
     L.sk = kt.dims[(size_t)kf].extent;
-    const int64_t qmul = f32 ? 32 : 64, kmul = f32 ? 32 : 64;
-    if (vt.dims[vc].extent != L.sk || L.sq % qmul != 0 || L.sk % kmul != 0 || L.sq == 0 || L.sk == 0) return false;
+    // 32 queries per wave and key blocks of 32 (both kernels)
+    if (vt.dims[vc].extent != L.sk || L.sq % 32 != 0 || L.sk % 32 != 0 || L.sq == 0 || L.sk == 0) return false;
     L.q_s = L.q.strides[(size_t)qf];
     L.k_s = L.k.strides[(size_t)kf];
     L.v_s = L.v.strides[vc];
@@ -1637,8 +1637,16 @@ class Planner {
       return;
     }
     int out = slots_.slot_of[pv] >= 0 ? slots_.slot_of[pv] : temp_slot(pv);
-    // waves per role: every role's share of a K / V tile (HD / 16 load instructions) must be whole
-    const int waves = L.sq % 256 == 0 && L.hd / 16 % 4 == 0 ? 4 : (L.sq % 128 == 0 ? 2 : 1);
+    // Waves per workgroup (32 queries each): eight (two per SIMD) when the queries divide, else the
+    // largest count that does, with two or more workgroups per CU; every wave's share of a K / V tile
+    // (HD / 16 load instructions) must be whole.
+    int waves = 1;
+    for (int w : {8, 4, 2}) {
+      if (L.sq % (32 * w) == 0 && (L.hd / 16) % w == 0) {
+        waves = w;
+        break;
+      }
+    }
     KernelWriter w(g_, slots_, "i64_t");
     std::string q = w.arg(L.q.slot, false), k = w.arg(L.k.slot, false), v = w.arg(L.v.slot, false),
                 o = w.arg(out, true);
@@ -1667,17 +1675,17 @@ class Planner {
       params += "const u16_t* __restrict__ " + x + ", ";
     }
     params += "u16_t* __restrict__ " + o;
-    src << "extern \"C\" __global__ void __launch_bounds__(" << 128 * waves << ") " << nm << "(" << params
+    src << "extern \"C\" __global__ void __launch_bounds__(" << 64 * waves << ") " << nm << "(" << params
         << ") {\n  accy::attn::flash<Cfg_" << nm << ">(" << q << ", " << k << ", " << v << ", " << o << ");\n}\n";
     KernelStep ks;
     ks.source = src.str();
     ks.name = nm;
     // Causal with an even number of query blocks: two complementary blocks per workgroup
     // (attn::blocks_per_group), so every workgroup streams the same number of keys.
-    const int64_t nqb = L.sq / (64 * waves);
+    const int64_t nqb = L.sq / (32 * waves);
     const int64_t pair = at.causal && nqb % 2 == 0 ? 2 : 1;
     ks.grid[0] = (uint32_t)(L.nb * nqb / pair);
-    ks.block[0] = 128 * waves;  // a scorer and an accumulator wave per 64 queries
+    ks.block[0] = 64 * waves;  // one wave per 32 queries
     ks.klass = "attention";
     ks.label = "attention:%" + std::to_string(pv);
     ks.algorithmic_flops = 4.0 * (double)L.nb * attention_pairs(at, L) * (double)L.hd;

@@ -197,7 +197,9 @@ def _scale(dtype):
 
 @pytest.mark.parametrize("heads,seq,dtype,causal", [
     (2, 256, "f16", False), (2, 256, "f16", True), (3, 384, "bf16", True), (1, 128, "bf16", False),
-    (2, 64, "f16", False), (1, 64, "f16", True)])
+    (2, 64, "f16", False), (1, 64, "f16", True),
+    # one-wave workgroups: a single key block (32 x 32), an odd number of causal query blocks
+    (1, 32, "f16", False), (2, 96, "bf16", True), (3, 160, "f16", False)])
 def test_fused_attention_matches_oracle(heads, seq, dtype, causal):
     say(f"attention {heads} x {seq} x 128 {dtype} causal={causal}")
     prog = W.attention_program(heads, seq, 128, dtype, causal)

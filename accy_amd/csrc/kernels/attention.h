@@ -208,16 +208,17 @@ __device__ __forceinline__ float sum_with_partner(float x) {
 // pairs, are the B operand of its P.V product as they stand). Two waves share each SIMD (one
 // workgroup of eight waves per CU, or two of four): each wave interleaves its own MFMAs with its
 // softmax VALU work, and the two waves take turns on the matrix core.
-// Step t of a query block (one workgroup barrier each, nkb + 2 steps), on K stage t % 4:
+// Step t of a query block (nkb + 2 steps), on K stage t % 4:
 //  * the MFMAs of S(t) (HD / 16, for t < nkb) alternate with those of P(t - 2).V(t - 2) (HD / 16,
 //    for t >= 2, V stage (t - 2) % 4);
-//  * the softmax of block t - 1 (for 1 <= t <= nkb) runs in 13 slots between them: slots 0-3 the
-//    row maximum, slot 4 the exchange with the partner lane and the decision whether the
-//    subtracted maximum moves, slots 5-12 exp2, packing and the row sum of one pair of scores each;
+//  * the softmax of block t - 1 (for 1 <= t <= nkb) runs between them, one pair of scores (exp2,
+//    packing, row sum) per slot, with the subtracted maximum of the earlier blocks; a check of the
+//    block's row sum then sends the rare block that moves the maximum to the exact path;
 //  * at the end of the step O is rescaled for block t - 1 when its maximum moved (rarely), between
 //    the P.V of block t - 2 and that of block t - 1;
-//  * K(t + 2) and V(t) are issued to their stages after the barrier, so both are two steps ahead
-//    of their use and every stage is rewritten only after the barrier that follows its last read.
+//  * even steps meet the workgroup at a barrier and then issue K(t + 2), K(t + 3), V(t) and
+//    V(t + 1) to their stages: every tile is issued at least two steps before its use, and every
+//    stage is rewritten only after the barrier that follows its last read.
 // What bounds it (C4 on MI355X): the chip's power limit. The MFMAs, the softmax's ~90 VALU
 // instructions per wave and step and the LDS reads add up to about the measured time, and the
 // clock drops as the work per cycle rises; every instruction removed from the loop counts.
@@ -261,42 +262,43 @@ struct Worker {
       if (8 * (r >> 2) + (r & 3) > th) s[PB][r] = -__builtin_inff();
   }
 
-  // Softmax, first part, for the block in score set PB, as slots 0-4 between the MFMAs: the row
-  // maximum in two max3 chains (slots 0-3), then (slot 4) the partner lane's half, the decision whether
-  // the subtracted maximum m moves (only when the new one exceeds it by more than 8) and the factor
-  // alpha for O and l. m starts at -FLT_MAX rather than -inf, so that s * SL - m is -inf exactly for
-  // the masked scores and no select is needed.
-  template <int PB, int T>
-  __device__ __forceinline__ void max_slot(float& ma, float& mb) {
-    const f32x16& sp = s[PB];
-    if constexpr (T == 0) {
-      ma = max3(sp[0], sp[1], sp[2]);
-      mb = max3(sp[3], sp[4], sp[5]);
-    } else if constexpr (T < 4) {
-      ma = max3(ma, sp[2 + 4 * T], sp[3 + 4 * T]);
-      mb = max3(mb, sp[4 + 4 * T], sp[5 + 4 * T]);
-    } else {
-      // T == 4: scores 14 and 15, then the exchange and the decision
-      const float mn = max_with_partner(max3(ma, mb, max3(sp[14], sp[15], sp[15]))) * C::SL;
-      const bool need = mn > m + 8.0f;
-      // branch-free, so that the step body stays one scheduling region
-      const float a = __builtin_amdgcn_exp2f(m - mn);
-      alpha[PB] = need ? a : 1.0f;
-      m = need ? mn : m;
-      l *= alpha[PB];
-    }
-  }
-
-  // Softmax, second part, for scores 2 j and 2 j + 1 of the block in set PB: P = exp2(s * SL - m),
-  // packed to 16 bits (the B operand of 16-key step j / 4), and the packed pair's exact sum into l.
+  // Softmax of the block in score set PB, for scores 2 j and 2 j + 1: P = exp2(s * SL - m) with the
+  // subtracted maximum m of the earlier blocks, packed to 16 bits (the B operand of 16-key step
+  // j / 4), and the packed pair's exact sum into ls, this lane's part of the block's row sum.
   template <int PB, int J>
-  __device__ __forceinline__ void pair(float ml) {
-    f32x16& sp = s[PB];
+  __device__ __forceinline__ void pair(float ml, float& ls) {
+    const f32x16& sp = s[PB];
     const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[2 * J], C::SL, ml));
     const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sp[2 * J + 1], C::SL, ml));
     const u32_t pr = pack2<C::DT>(e0, e1);
     p[PB][J >> 2][J & 3] = pr;
-    l = add_pair<C::DT>(pr, l);
+    ls = add_pair<C::DT>(pr, ls);
+  }
+
+  // The lazy maximum. m moves only when a block's maximum exceeds it by more than 8 (a factor 256),
+  // so P stays <= 256. The exponentials are computed first with the old m; a lane whose block sum
+  // stays <= 256 has every P <= 256, and when every lane's does (the common case) nothing else is
+  // needed. Otherwise this takes the row maximum (two max3 chains, then the partner lane's half),
+  // moves m where it must, sets alpha (the factor for O and l) and recomputes the block. m starts
+  // at -FLT_MAX, so the first block always comes here (its exponentials overflow), and
+  // s * SL - m is -inf exactly for the masked scores.
+  template <int PB>
+  __device__ __forceinline__ void exact_block(float& ls) {
+    const f32x16& sp = s[PB];
+    float a = max3(sp[0], sp[1], sp[2]), b = max3(sp[3], sp[4], sp[5]);
+    a = max3(a, sp[6], sp[7]);
+    b = max3(b, sp[8], sp[9]);
+    a = max3(a, sp[10], sp[11]);
+    b = max3(b, sp[12], sp[13]);
+    a = max3(a, sp[14], sp[15]);
+    const float mn = max_with_partner(max3(a, b, b)) * C::SL;
+    const bool need = mn > m + 8.0f;
+    if (__any(need)) {
+      alpha[PB] = need ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+      m = need ? mn : m;
+      ls = 0.0f;
+      For<0, 8>::run([&](auto ji) { pair<PB, decltype(ji)::value>(-m, ls); });
+    }
   }
 
   // Step t on K stage ST = t % 4: S(t) when HS, the softmax of block t - 1 when HM, P.V of block
@@ -305,13 +307,16 @@ struct Worker {
   __device__ __forceinline__ void step(long t, long nkb) {
     constexpr int SB = ST & 1, PB = SB ^ 1, NE = (HS ? DS : 0) + (HP ? NPV : 0);
     constexpr int VST = (ST + 2) & 3;
-    // K(t) and V(t - 2) were issued at step t - 2; K(t + 1) and V(t - 1) at step t - 1 may still fly.
-    if (t + 1 < nkb) gemm::wait_vmcnt<2 * PER>();
-    else if (t - 1 < nkb) gemm::wait_vmcnt<PER>();
-    else gemm::wait_vmcnt<0>();
-    gemm::lds_reads_done_barrier();
-    if (t + 2 < nkb) dma_share<PER>(kb, (t + 2) * BK * C::K_S, off.kg, sh.ks[(ST + 2) & 3], wave);
-    if (t < nkb) dma_share<PER>(vb, t * BK * C::V_S, off.vg, sh.vs[ST], wave);
+    if constexpr ((ST & 1) == 0) {
+      // Even steps meet the workgroup: every load in flight (issued at step t - 2: K(t), K(t + 1),
+      // V(t - 2), V(t - 1)) is complete and the stages read at steps t - 2 and t - 1 are free.
+      gemm::wait_vmcnt<0>();
+      gemm::lds_reads_done_barrier();
+      if (t + 2 < nkb) dma_share<PER>(kb, (t + 2) * BK * C::K_S, off.kg, sh.ks[(ST + 2) & 3], wave);
+      if (t + 3 < nkb) dma_share<PER>(kb, (t + 3) * BK * C::K_S, off.kg, sh.ks[(ST + 3) & 3], wave);
+      if (t < nkb) dma_share<PER>(vb, t * BK * C::V_S, off.vg, sh.vs[ST], wave);
+      if (t + 1 < nkb) dma_share<PER>(vb, (t + 1) * BK * C::V_S, off.vg, sh.vs[(ST + 1) & 3], wave);
+    }
     if constexpr (HM)
       if constexpr (C::CAUSAL) mask<PB>((t - 1) * BK);
 
@@ -325,18 +330,11 @@ struct Worker {
     }
     if constexpr (HP)
       For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < NPV) vf[i] = v_frag<HD>(vl, off.vf[i / 2], i % 2); });
-    // The softmax of block t - 1 as 13 slots: max slots 0-4, then pairs 0-7 (slot 5 + j). Slot 0 runs
-    // while the first fragments arrive, the others between the MFMAs.
-    float ma, mb, ml = 0.0f;
-    auto slot = [&](auto ci) {
-      constexpr int c = decltype(ci)::value;
-      if constexpr (c < 5) {
-        max_slot<PB, c>(ma, mb);
-        if constexpr (c == 4) ml = -m;
-      } else {
-        pair<PB, c - 5>(ml);
-      }
-    };
+    // The softmax of block t - 1: pair 0 while the first fragments arrive, pairs 1-7 between the
+    // MFMAs, then the check of the lazy maximum.
+    const float ml = -m;
+    float ls = 0.0f;
+    auto slot = [&](auto ji) { pair<PB, decltype(ji)::value>(ml, ls); };
     if constexpr (HM) slot(Int<0>{});
     __builtin_amdgcn_sched_barrier(0);
     For<0, NE>::run([&](auto ei) {
@@ -353,11 +351,14 @@ struct Worker {
         o[i / 2] = gemm::mfma32x32x16<C::DT>(vf[i % (PF + 1)], p[SB][i % 2], o[i / 2]);
       }
       __builtin_amdgcn_sched_barrier(0);
-      if constexpr (HM) For<1 + e * 12 / NE, 1 + (e + 1) * 12 / NE>::run(slot);
+      if constexpr (HM) For<1 + e * 7 / NE, 1 + (e + 1) * 7 / NE>::run(slot);
       __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (HM) {
-      if constexpr (NE == 0) For<1, 13>::run(slot);
+      if constexpr (NE == 0) For<1, 8>::run(slot);
+      alpha[PB] = 1.0f;
+      if (__any(!(ls <= 256.0f))) exact_block<PB>(ls);
+      l = l * alpha[PB] + ls;
       // The softmax results are consumed here, so that no pass sinks their VALU work past the next
       // barrier (out of the MFMA slots it was placed in).
       asm volatile("" : "+v"(p[PB][0]), "+v"(p[PB][1]), "+v"(l), "+v"(alpha[PB]));
@@ -382,10 +383,6 @@ struct Worker {
     off.init(wave, lane);
     dma_share<PER>(kb, 0, off.kg, sh.ks[0], wave);
     if (nkb > 1) dma_share<PER>(kb, BK * C::K_S, off.kg, sh.ks[1], wave);
-    // Step 0 waits for K(0) only (K(1) may fly); the general rule below counts K(1) as issued at
-    // step -1.
-    if (nkb > 1) gemm::wait_vmcnt<PER>();
-    else gemm::wait_vmcnt<0>();
     step0(nkb);
     if (nkb == 1) {
       step<1, false, true, false>(1, nkb);
@@ -449,11 +446,14 @@ struct Worker {
       }
   }
 
-  // Step 0: barrier, K(2) and V(0) issued, S(0).
+  // Step 0: K(0) and K(1) complete, barrier, K(2), K(3), V(0) and V(1) issued, S(0).
   __device__ __forceinline__ void step0(long nkb) {
+    gemm::wait_vmcnt<0>();
     gemm::lds_reads_done_barrier();
     if (2 < nkb) dma_share<PER>(kb, 2 * BK * C::K_S, off.kg, sh.ks[2], wave);
+    if (3 < nkb) dma_share<PER>(kb, 3 * BK * C::K_S, off.kg, sh.ks[3], wave);
     dma_share<PER>(vb, 0, off.vg, sh.vs[0], wave);
+    if (1 < nkb) dma_share<PER>(vb, BK * C::V_S, off.vg, sh.vs[1], wave);
     const u16_t* kl = sh.ks[0];
     u32x4 kf[3];
     kf[0] = k_frag(kl, off.kf[0]);
@@ -476,7 +476,7 @@ constexpr long blocks_per_group() {
   return C::CAUSAL && NQB % 2 == 0 ? 2 : 1;
 }
 
-// One query block (queries qb * 32 * WAVES ...) of batch index b. Every wave meets nkb + 2
+// One query block (queries qb * 32 * WAVES ...) of batch index b. Every wave meets the same
 // barriers, so blocks can follow each other.
 template <class C>
 __device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __restrict__ Q, const u16_t* __restrict__ K,

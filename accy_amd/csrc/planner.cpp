@@ -1583,11 +1583,11 @@ class Planner {
     const int vf = free_axis(vt.rank(), d.rhs_batch, d.rhs_contract);
     if (qf < 0 || kf < 0 || vf < 0 || d.rhs_contract.size() != 1) return false;
     const size_t qc = (size_t)qk.lhs_contract[0], kc = (size_t)qk.rhs_contract[0], vc = (size_t)d.rhs_contract[0];
-    // Head dimension (Q.K contraction and V's free axis, unit stride): 64 or 128 for 16-bit operands
-    // (attn::flash), 64 for f32 (attn::flash_f32, the reference's flash pattern).
+    // Head dimension (Q.K contraction and V's free axis, unit stride): 64, 128 or 256 for 16-bit
+    // operands (attn::flash), 64 for f32 (attn::flash_f32, the reference's flash pattern).
     const bool f32 = d.result.dtype == DType::f32;
     L.hd = qt.dims[qc].extent;
-    if ((L.hd != 128 || f32) && L.hd != 64) return false;
+    if (f32 ? L.hd != 64 : (L.hd != 64 && L.hd != 128 && L.hd != 256)) return false;
     if (kt.dims[kc].extent != L.hd || vt.dims[(size_t)vf].extent != L.hd) return false;
     if (L.q.strides[qc] != 1 || L.k.strides[kc] != 1 || L.v.strides[(size_t)vf] != 1) return false;
     L.sq = qt.dims[(size_t)qf].extent;
@@ -1639,9 +1639,11 @@ class Planner {
     int out = slots_.slot_of[pv] >= 0 ? slots_.slot_of[pv] : temp_slot(pv);
     // Waves per workgroup (32 queries each): eight (two per SIMD) when the queries divide, else the
     // largest count that does, with two or more workgroups per CU; every wave's share of a K / V tile
-    // (HD / 16 load instructions) must be whole.
+    // (HD / 16 load instructions) must be whole. Head dimension 256 takes at most four (one wave per
+    // SIMD: its O and Q^T alone fill 192 registers, and its K / V stages 128 KiB of LDS).
     int waves = 1;
     for (int w : {8, 4, 2}) {
+      if (L.hd == 256 && w > 4) continue;
       if (L.sq % (32 * w) == 0 && (L.hd / 16) % w == 0) {
         waves = w;
         break;

@@ -408,6 +408,17 @@ def test_fused_16bit_attention_head_dim_64(heads, seq, dtype, causal):
                      exact_attention(*ins, scale, causal, dtype))
 
 
+@pytest.mark.parametrize("heads,seq,dtype,causal", [(2, 256, "f16", False), (2, 384, "bf16", True), (1, 96, "bf16", False)])
+def test_fused_16bit_attention_head_dim_256(heads, seq, dtype, causal):
+    """Head dimension 256: one wave per SIMD (four-wave workgroups, 128 KiB of K / V stages)."""
+    say(f"{dtype} attention {heads} x {seq} x 256 causal={causal}")
+    prog = W.attention_program(heads, seq, 256, dtype, causal=causal)
+    assert "accy::attn::flash<" in hip.plan_source(prog)
+    ins = W.attention_inputs(heads, seq, 256, dtype, seed=5 * heads + seq)
+    scale = float(to_f32(W.to_dtype(np.array([1 / math.sqrt(256)]), dtype), dtype)[0])
+    assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype,
+                     exact_attention(*ins, scale, causal, dtype))
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_gemm_mulsum_16bit_on_mfma(dtype):
     say(f"gemm {dtype} 256x256x512 mulsum")

@@ -7,6 +7,7 @@
 #include <cstring>
 #include <memory>
 #include <optional>
+#include <functional>
 #include <set>
 #include <sstream>
 
@@ -1942,6 +1943,31 @@ class Planner {
     return true;
   }
 
+  // A fused epilogue worth a lookup table: contraction and result both 16-bit, and the result a chain
+  // of at least six elementwise operations whose leaves are the contraction value and splat float
+  // constants only (no other tensor, no index), so it is a function of the rounded contraction value.
+  bool lut_epilogue(uint32_t v, uint32_t target, DType d, DType td) const {
+    auto b16 = [](DType t) { return t == DType::bf16 || t == DType::f16; };
+    if (!b16(d) || !b16(td) || target == v || std::getenv("ACCY_GEMM_NO_LUT")) return false;
+    std::set<uint32_t> seen;
+    int ops = 0;
+    std::function<bool(uint32_t)> ok = [&](uint32_t x) -> bool {
+      if (x == v || seen.count(x)) return true;
+      double c;
+      if (splat_float(x, c)) return true;
+      const Op& o = g_.ops[x];
+      const bool ew = o.kind == Kind::unary || o.kind == Kind::binary || o.kind == Kind::select ||
+                      o.kind == Kind::compare;
+      if (!ew) return false;
+      seen.insert(x);
+      ++ops;
+      for (uint32_t a : o.args)
+        if (!ok(a)) return false;
+      return true;
+    };
+    return ok(target) && ops >= 6;
+  }
+
   // Writes the contraction described by gs into the slot of value v (laid out per os), or, with a
   // fused epilogue, the value that the elementwise region after v materialises.
   void gemm(uint32_t v, const GemmShape& gs, const OutStrides& os) {
@@ -1977,9 +2003,46 @@ class Planner {
           out = "vv";
           return true;
         };
-        std::string x = w->value(target, coords, sc);
-        int out = slots_.slot_of[target] >= 0 ? slots_.slot_of[target] : temp_slot(target);
-        epi << sc.indent << w->store(out, cidx, g_.type(target).dtype, x) << "\n";
+        const DType td = g_.type(target).dtype;
+        if (lut_epilogue(v, target, d, td)) {
+          // A 16-bit epilogue that is a function of the rounded contraction value alone: a table
+          // kernel evaluates the same generated expression for all 65536 bit patterns, and the
+          // contraction's epilogue is one lookup per element (bit-identical by construction).
+          const int tslot = slots_.add(SlotInfo::Temp, -1, td, 65536u * 2u);
+          KernelWriter tw(g_, slots_, "i64_t");
+          tw.arg(tslot, true);
+          std::ostringstream tk;
+          Scope tsc(tk, "  ");
+          tw.provide = [&](uint32_t vid, const std::vector<std::string>&, std::string& out) -> bool {
+            if (vid != v) return false;
+            out = "vv";
+            return true;
+          };
+          const std::string tx = tw.value(target, coords, tsc);
+          const std::string tnm = name("lut", target);
+          std::ostringstream tsrc;
+          tsrc << "extern \"C\" __global__ void __launch_bounds__(256) " << tnm << "(" << tw.params() << ") {\n"
+               << "  const int i = (int)(blockIdx.x * 256 + threadIdx.x);\n"
+               << "  const float vv = " << (d == DType::bf16 ? "accy::bf16_to_f32" : "accy::f16_to_f32") << "((u16_t)i);\n"
+               << tk.str() << "  " << tw.store(tslot, "i", td, tx) << "\n}\n";
+          KernelStep ts;
+          ts.source = tsrc.str();
+          ts.name = tnm;
+          ts.grid[0] = 256;
+          ts.block[0] = 256;
+          ts.klass = "lut";
+          ts.label = "lut:%" + std::to_string(target);
+          const std::string tab = w->arg(tslot, false);
+          int out = slots_.slot_of[target] >= 0 ? slots_.slot_of[target] : temp_slot(target);
+          const std::string dst = w->arg(out, true);
+          epi << "    " << dst << "[" << cidx << "] = " << tab << "["
+              << (d == DType::bf16 ? "accy::f32_to_bf16(v)" : "accy::f32_to_f16(v)") << "];\n";
+          push(std::move(ts), tw);
+        } else {
+          std::string x = w->value(target, coords, sc);
+          int out = slots_.slot_of[target] >= 0 ? slots_.slot_of[target] : temp_slot(target);
+          epi << sc.indent << w->store(out, cidx, td, x) << "\n";
+        }
       } catch (const NotFusable&) {
         target = v;
         w.reset();

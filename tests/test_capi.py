@@ -72,6 +72,14 @@ def test_attention_fusion_decision(prog, fused):
         assert src.count("accy::attn::flash<") + src.count("accy::attn::flash_f32<") == 1
 
 
+def test_decoder_gelu_epilogue_is_a_lookup_table():
+    """The decoder's MLP-up contraction ends in GELU (ten bf16 operations on the contraction value and
+    constants): a table kernel evaluates them once per 16-bit pattern and the epilogue looks them up;
+    the contractions whose epilogues read other tensors (the residual adds) keep direct epilogues."""
+    src = hip.plan_source(W.decoder_program(1, 256, 512, 4, 128, 1024), compile=False)
+    assert src.count("accy_lut_") == 1 and "// lut:%" in src
+    assert src.count("[accy::f32_to_bf16(v)]") == 1
+
 def test_attention_fusion_keeps_values_read_elsewhere():
     # the probabilities are also an output, so they must be materialised: no fusion
     def body(b, a):

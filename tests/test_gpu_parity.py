@@ -253,6 +253,38 @@ def test_grouped_projections_equal_separate_launches():
     assert_rowwise(grouped, oracle_run(prog, ins)[0], 2e-2, "bf16")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_epilogue_lookup_table_equals_direct_epilogue(dtype):
+    """A 16-bit contraction whose fused epilogue is a chain of elementwise operations on the contraction
+    value and splat constants (here GELU's tanh form, ten operations) runs that chain once per 16-bit
+    pattern in a table kernel and looks the result up per element. The outputs equal the directly
+    evaluated epilogue (ACCY_GEMM_NO_LUT) bit for bit, and match the oracle."""
+    import os
+    m, k, n = 512, 256, 768
+    specs = [T.spec(dtype, m=m, k=k), T.spec(dtype, k=k, n=n)]
+    scalar = T.Type(dtype, ())
+
+    def body(b, a):
+        x = a[0].contract(a[1], "k")
+        c = lambda f: b.full_float(scalar, f)
+        inner = x.add(x.mul(x).mul(x).mul(c(0.044715))).mul(c(0.7978845608028654))
+        return [x.mul(c(0.5)).mul(inner.tanh().add(c(1.0)))]
+
+    prog = T.define("gelu_" + dtype, specs, body)
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "accy_lut_" in src and "f32_to_" in src
+    rng = np.random.default_rng(21)
+    ins = [W.to_dtype(rng.standard_normal((m, k)), dtype), W.to_dtype(rng.standard_normal((k, n)) / 8, dtype)]
+    table = hip_run(prog, ins)[0]
+    os.environ["ACCY_GEMM_NO_LUT"] = "1"
+    try:
+        assert "accy_lut_" not in hip.plan_source(prog.encode(), compile=False)
+        direct = hip_run(prog, ins)[0]
+    finally:
+        del os.environ["ACCY_GEMM_NO_LUT"]
+    assert np.array_equal(np.asarray(table).view(np.uint8), np.asarray(direct).view(np.uint8))
+    assert_rowwise(table, oracle_run(prog, ins)[0], 2e-2, dtype)
+
 def test_decoder_with_fused_causal_attention():
     say("decoder 1 x 128 x 256, 2 heads x 128, ffn 512, bf16")
     prog = W.decoder_program(1, 128, 256, 2, 128, 512, dtype="bf16")

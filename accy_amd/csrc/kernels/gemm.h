@@ -493,6 +493,12 @@ struct DmaGroup {
   }
 };
 
+// Epilogue functors with a lookup table declare `static constexpr bool kTable = true`, a member
+// table() (65536 16-bit results in global memory), index(v) (the bit pattern of the rounded
+// contraction value) and put(batch, m, n, bits); others are called as epi(batch, m, n, v).
+template <class E, class = void> struct HasTable { static constexpr bool value = false; };
+template <class E> struct HasTable<E, decltype((void)E::kTable)> { static constexpr bool value = E::kTable; };
+
 // Requires K % 32 == 0 with at least STAGES K steps and 16-byte aligned rows (M or N not a multiple
 // of the tile: see dma_part);
 // 256 threads (2 x 2 waves). LDS: STAGES x (BM + BN) x 64 bytes (STAGES = 4 with a 256 x 256 tile:
@@ -557,17 +563,76 @@ __device__ __forceinline__ void mma16_dma_tile(const u16_t* __restrict__ A, cons
 
   const long col_base = n0 + wn * (BN / 2) + (lane & 31);
   const long row_base = m0 + wm * (BM / 2) + (lane >> 5) * 4;
+  auto each = [&](auto f) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const long m = row_base + i * 32 + g * 8 + r, n = col_base + j * 32;
-          if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) epi(batch, m, n, acc[i][j][g * 4 + r]);
+          for (int r = 0; r < 4; ++r) {
+            const long m = row_base + i * 32 + g * 8 + r, n = col_base + j * 32;
+            if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) f(m, n, acc[i][j][g * 4 + r]);
+          }
+  };
+  if constexpr (HasTable<Epi>::value) {
+    // A table epilogue (65536 16-bit results indexed by the rounded contraction value): with four
+    // stages of 256 x 256 tiles the eight 16 KiB stage arrays are the kernel's whole 128 KiB of LDS,
+    // i.e. they tile LDS addresses [0, 128 KiB) in some order. After the last K step each array
+    // receives the table entries of its own addresses, and the lookups read LDS address 2 x index
+    // (ds_read_u16 written as assembly, 16 per wait, since the compiler's view of the arrays ends
+    // at each one's bounds). Otherwise the table is read from global memory (L2).
+    const u16_t* __restrict__ table = epi.table();
+    bool in_lds = false;
+    auto at = [](const u16_t* p) { return (u32_t)(unsigned long)(const ACCY_LDS u16_t*)p; };
+    if constexpr (S == 4 && A_ST == 8192 && B_ST == 8192) {
+      constexpr u32_t LAST = 131072 - 16384;
+      in_lds = at(a0) <= LAST && at(a1) <= LAST && at(a2) <= LAST && at(a3) <= LAST && at(b0) <= LAST &&
+               at(b1) <= LAST && at(b2) <= LAST && at(b3) <= LAST;
+    }
+    if (in_lds) {
+      lds_reads_done_barrier();
+      // each wave fills two arrays (16 KiB each, 16 instructions of 1 KiB)
+      auto fill = [&](u16_t* dst) {
+        const u16_t* const src = table + at(dst) / 2;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dma16(src + i * 512 + lane * 8, (ACCY_LDS void*)(dst + i * 512));
+      };
+      switch (__builtin_amdgcn_readfirstlane(wave)) {
+        case 0: fill(a0); fill(a1); break;
+        case 1: fill(a2); fill(a3); break;
+        case 2: fill(b0); fill(b1); break;
+        default: fill(b2); fill(b3); break;
+      }
+      wait_vmcnt<0>();
+      lds_reads_done_barrier();
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          u32_t bits[16];
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const u32_t addr = 2u * (u32_t)Epi::index(acc[i][j][e]);
+            asm volatile("ds_read_u16 %0, %1" : "=v"(bits[e]) : "v"(addr));
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)"
+                       : "+v"(bits[0]), "+v"(bits[1]), "+v"(bits[2]), "+v"(bits[3]), "+v"(bits[4]), "+v"(bits[5]),
+                         "+v"(bits[6]), "+v"(bits[7]), "+v"(bits[8]), "+v"(bits[9]), "+v"(bits[10]), "+v"(bits[11]),
+                         "+v"(bits[12]), "+v"(bits[13]), "+v"(bits[14]), "+v"(bits[15]));
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const long m = row_base + i * 32 + (e >> 2) * 8 + (e & 3), n = col_base + j * 32;
+            if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) epi.put(batch, m, n, (u16_t)bits[e]);
+          }
         }
+    } else {
+      each([&](long m, long n, float v) { epi.put(batch, m, n, table[Epi::index(v)]); });
+    }
+  } else {
+    each([&](long m, long n, float v) { epi(batch, m, n, v); });
+  }
 }
 
 template <class C, class Epi>

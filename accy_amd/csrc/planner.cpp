@@ -1979,6 +1979,7 @@ class Planner {
     uint32_t target = v;
     std::unique_ptr<KernelWriter> w;
     std::ostringstream epi;
+    std::string table_members;  // a lookup-table epilogue's interface (gemm.h HasTable)
     // The fused epilogue (dot_general results only: os is their row-major layout).
     const bool rowmajor = os.b == gs.m * gs.n && os.m == gs.n && os.n == 1;
     if (op.kind == Kind::dot_general && rowmajor && epilogue_target(v, target)) {
@@ -2035,8 +2036,13 @@ class Planner {
           const std::string tab = w->arg(tslot, false);
           int out = slots_.slot_of[target] >= 0 ? slots_.slot_of[target] : temp_slot(target);
           const std::string dst = w->arg(out, true);
-          epi << "    " << dst << "[" << cidx << "] = " << tab << "["
-              << (d == DType::bf16 ? "accy::f32_to_bf16(v)" : "accy::f32_to_f16(v)") << "];\n";
+          const std::string idx = d == DType::bf16 ? "accy::f32_to_bf16(v)" : "accy::f32_to_f16(v)";
+          epi << "    " << dst << "[" << cidx << "] = " << tab << "[" << idx << "];\n";
+          table_members = "  static constexpr bool kTable = true;\n"
+                          "  __device__ __forceinline__ const u16_t* table() const { return " + tab + "; }\n"
+                          "  static __device__ __forceinline__ u16_t index(float v) { return " + idx + "; }\n"
+                          "  __device__ __forceinline__ void put(long b, long m, long n, u16_t bits) const { " +
+                          dst + "[" + cidx + "] = bits; }\n";
           push(std::move(ts), tw);
         } else {
           std::string x = w->value(target, coords, sc);
@@ -2076,8 +2082,10 @@ class Planner {
     KernelStep k;
     src << "#include \"gemm\"\n";
     src << "struct Epi_" << nm << " {\n" << members.str()
+        << table_members
         << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
-        << (target != v ? "    const float vv = " + round_to(d, "v") + ";\n" : "") << epi.str() << "  }\n};\n";
+        << (target != v && table_members.empty() ? "    const float vv = " + round_to(d, "v") + ";\n" : "") << epi.str()
+        << "  }\n};\n";
     if (d == DType::f32) {
       // f32 on v_mfma_f32_32x32x2_f32: exact 256 x 256 x 32 tiles (gemm_eligible checked the layout).
       src << "struct Cfg_" << nm << " {\n"

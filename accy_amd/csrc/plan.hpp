@@ -45,6 +45,9 @@ struct KernelStep {
   std::string tuning_key;
   uint32_t candidate_count = 1;
   uint32_t candidate = 0;
+  // The kernel's output depends on constants only (a lookup table): it runs on an executor's first
+  // invocation, whose temporaries persist, and on every scratch-bound one.
+  bool once = false;
 };
 
 struct CopyStep {

@@ -2033,6 +2033,7 @@ class Planner {
           ts.block[0] = 256;
           ts.klass = "lut";
           ts.label = "lut:%" + std::to_string(target);
+          ts.once = true;
           const std::string tab = w->arg(tslot, false);
           int out = slots_.slot_of[target] >= 0 ? slots_.slot_of[target] : temp_slot(target);
           const std::string dst = w->arg(out, true);

@@ -259,6 +259,7 @@ const std::vector<KernelTiming>& Executor::timings() {
     for (size_t c = 0; c < n; ++c) {
       float ms = 0;
       check(hipEventElapsedTime(&ms, events_[(c * nk + k) * 2], events_[(c * nk + k) * 2 + 1]), "hipEventElapsedTime");
+      if (skipped_[c * nk + k]) ms = 0.0f;
       sum += ms;
       if (c == last) timings_[k].last_ms = ms;
     }
@@ -277,14 +278,17 @@ void Executor::run_steps(hipStream_t stream, uint8_t* scratch) {
   // Event slot of this invocation when profiling (created on first use; never with scratch).
   const size_t nk = timings_.size();
   hipEvent_t* ev = nullptr;
+  uint8_t* skipped = nullptr;  // per kernel of this invocation: a run-once kernel skipped (0 ms)
   if (profiling_ && nk && !scratch) {
     const size_t slot = recorded_ % kProfiledCalls;
     if (events_.size() < (slot + 1) * nk * 2) {
       size_t old = events_.size();
       events_.resize((slot + 1) * nk * 2, nullptr);
+      skipped_.resize((slot + 1) * nk, 0);
       for (size_t e = old; e < events_.size(); ++e) check(hipEventCreate(&events_[e]), "hipEventCreate");
     }
     ev = &events_[slot * nk * 2];
+    skipped = &skipped_[slot * nk];
   }
   size_t ki = 0;
   for (size_t i = 0; i < plan_.steps.size(); ++i) {
@@ -300,6 +304,19 @@ void Executor::run_steps(hipStream_t stream, uint8_t* scratch) {
       continue;
     }
     const KernelStep& k = st.kernel;
+    if (k.once && !scratch) {
+      if (once_done_.size() != plan_.steps.size()) once_done_.assign(plan_.steps.size(), false);
+      if (once_done_[i]) {
+        if (ev) {
+          check(hipEventRecord(ev[2 * ki], stream), "hipEventRecord");
+          check(hipEventRecord(ev[2 * ki + 1], stream), "hipEventRecord");
+          skipped[ki] = 1;
+        }
+        ++ki;
+        continue;
+      }
+    }
+    if (skipped) skipped[ki] = 0;
     std::vector<void*> ptrs(k.args.size());
     std::vector<void*> params(k.args.size());
     for (size_t a = 0; a < k.args.size(); ++a) {
@@ -310,6 +327,7 @@ void Executor::run_steps(hipStream_t stream, uint8_t* scratch) {
     check(hipModuleLaunchKernel(fn_[i], k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2],
                                 k.shared_bytes, stream, params.data(), nullptr),
           "hipModuleLaunchKernel");
+    if (k.once && !scratch) once_done_[i] = true;
     if (ev) check(hipEventRecord(ev[2 * ki + 1], stream), "hipEventRecord");
     ++ki;
   }

@@ -88,6 +88,8 @@ class Executor {
   std::vector<void*> owned_;     // device allocation per slot (Temp / Const; staging for Input / Output)
   std::vector<void*> bound_;     // pointer used for each slot during a run
   std::vector<hipFunction_t> fn_;
+  std::vector<bool> once_done_;    // per step: a run-once kernel has run (KernelStep::once)
+  std::vector<uint8_t> skipped_;   // per profiled call and kernel: a run-once kernel was skipped
   hipStream_t stream_ = nullptr;
   bool profiling_ = false;
   bool pending_ = false;           // recorded events not yet read back

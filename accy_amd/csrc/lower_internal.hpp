@@ -1,4 +1,4 @@
-// Internals shared by the planner (planner.cpp) and the expression code generator (lower.cpp).
+// Internals shared by the planner (planner*.cpp) and the expression code generator (lower.cpp).
 #pragma once
 
 #include <functional>

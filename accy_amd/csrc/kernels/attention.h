@@ -302,22 +302,27 @@ struct Worker {
     }
   }
 
+  // Even step t (K stage ST = t % 4) meets the workgroup: every load in flight (issued at step
+  // t - 2: K(t), K(t + 1), V(t - 2), V(t - 1)) is complete and the stages read at steps t - 2 and
+  // t - 1 are free; then this wave's share of K(t + 2), K(t + 3), V(t) and V(t + 1) is issued (tiles
+  // up to the workgroup's key block count nkb).
+  template <int ST>
+  __device__ __forceinline__ void meet(long t, long nkb) {
+    gemm::wait_vmcnt<0>();
+    gemm::lds_reads_done_barrier();
+    if (t + 2 < nkb) dma_share<PER>(kb, (t + 2) * BK * C::K_S, off.kg, sh.ks[(ST + 2) & 3], wave);
+    if (t + 3 < nkb) dma_share<PER>(kb, (t + 3) * BK * C::K_S, off.kg, sh.ks[(ST + 3) & 3], wave);
+    if (t < nkb) dma_share<PER>(vb, t * BK * C::V_S, off.vg, sh.vs[ST], wave);
+    if (t + 1 < nkb) dma_share<PER>(vb, (t + 1) * BK * C::V_S, off.vg, sh.vs[(ST + 1) & 3], wave);
+  }
+
   // Step t on K stage ST = t % 4: S(t) when HS, the softmax of block t - 1 when HM, P.V of block
   // t - 2 when HP. Score sets, P sets and factors of block j live at index j % 2.
   template <int ST, bool HS, bool HM, bool HP>
   __device__ __forceinline__ void step(long t, long nkb) {
     constexpr int SB = ST & 1, PB = SB ^ 1, NE = (HS ? DS : 0) + (HP ? NPV : 0);
     constexpr int VST = (ST + 2) & 3;
-    if constexpr ((ST & 1) == 0) {
-      // Even steps meet the workgroup: every load in flight (issued at step t - 2: K(t), K(t + 1),
-      // V(t - 2), V(t - 1)) is complete and the stages read at steps t - 2 and t - 1 are free.
-      gemm::wait_vmcnt<0>();
-      gemm::lds_reads_done_barrier();
-      if (t + 2 < nkb) dma_share<PER>(kb, (t + 2) * BK * C::K_S, off.kg, sh.ks[(ST + 2) & 3], wave);
-      if (t + 3 < nkb) dma_share<PER>(kb, (t + 3) * BK * C::K_S, off.kg, sh.ks[(ST + 3) & 3], wave);
-      if (t < nkb) dma_share<PER>(vb, t * BK * C::V_S, off.vg, sh.vs[ST], wave);
-      if (t + 1 < nkb) dma_share<PER>(vb, (t + 1) * BK * C::V_S, off.vg, sh.vs[(ST + 1) & 3], wave);
-    }
+    if constexpr ((ST & 1) == 0) meet<ST>(t, nkb);
     if constexpr (HM)
       if constexpr (C::CAUSAL) mask<PB>((t - 1) * BK);
 
@@ -372,8 +377,11 @@ struct Worker {
     }
   }
 
-  // One query block: prologue (Q^T into registers, K(0) and K(1) issued), nkb + 2 steps, epilogue.
-  __device__ __forceinline__ void run(const u16_t* __restrict__ qp, u16_t* __restrict__ out, long b, long nkb) {
+  // One query block: prologue (Q^T into registers, K(0) and K(1) issued), nkc + 2 steps over this
+  // wave's key blocks, epilogue, then the workgroup's remaining steps (nkb - nkc = 0 or 4; key
+  // blocks that are masked for every query of this wave) only meet the workgroup and issue loads.
+  __device__ __forceinline__ void run(const u16_t* __restrict__ qp, u16_t* __restrict__ out, long b, long nkb,
+                                      long nkc) {
 #pragma unroll
     for (int dd = 0; dd < DS; ++dd) qf[dd] = *(const u32x4*)(qp + query() * C::Q_S + 16 * dd + 8 * (lane >> 5));
 #pragma unroll
@@ -389,17 +397,22 @@ struct Worker {
       step<1, false, true, false>(1, nkb);
       step<2, false, false, true>(2, nkb);
     } else {
-      steps(nkb);
+      steps(nkb, nkc);
     }
     epilogue(out, b);
+    if (nkc < nkb) {
+      // nkc = 0 (mod 4): the remaining even steps are nkc + 2 and nkc + 4
+      meet<2>(nkc + 2, nkb);
+      meet<0>(nkc + 4, nkb);
+    }
   }
 
-  // Steps 1 .. nkb + 1 for nkb >= 2. The steady-state loop leaves t = 2 (mod 4), so the stage of
-  // every remaining step is known; r = nkb - t scored steps remain (0 .. 3).
-  __device__ __forceinline__ void steps(long nkb) {
+  // Steps 1 .. nkc + 1 for nkc >= 2 (loads up to nkb). The steady-state loop leaves t = 2 (mod 4),
+  // so the stage of every remaining step is known; r = nkc - t scored steps remain (0 .. 3).
+  __device__ __forceinline__ void steps(long nkb, long nkc) {
     step<1, true, true, false>(1, nkb);
     long t = 2;
-    for (; t + 3 < nkb; t += 4) {
+    for (; t + 3 < nkc; t += 4) {
       step<2, true, true, true>(t, nkb);
       step<3, true, true, true>(t + 1, nkb);
       step<0, true, true, true>(t + 2, nkb);
@@ -409,7 +422,7 @@ struct Worker {
     // and key counts that are multiples of 128); then only that tail is compiled.
     constexpr long BQ = 32 * WAVES, NKB = C::SK / BK;
     constexpr int MOD = !C::CAUSAL ? (int)((NKB - 2) % 4) : (BQ % 128 == 0 && C::SK % 128 == 0 ? 2 : -1);
-    const long r = MOD >= 0 ? MOD : nkb - t;
+    const long r = MOD >= 0 ? MOD : nkc - t;
     if (r == 0) {
       step<2, false, true, true>(t, nkb);
       step<3, false, false, true>(t + 1, nkb);
@@ -496,7 +509,15 @@ __device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __res
   f.q0 = q0;
   f.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   f.lane = (int)(threadIdx.x & 63);
-  f.run(Q + C::q_off(b), O, b, nkb);
+  // Under the causal mask the last four key blocks of a 256-query block lie above the diagonal for
+  // every query of waves 0-3 (queries q0 .. q0 + 127) when the block's keys reach its last query:
+  // those waves skip their work and only meet the workgroup there. With waves w and w + 4 on one
+  // SIMD, each SIMD then carries 12 instead of 16 wave-steps over the diagonal. (Only where the
+  // loop tail is fixed at compile time: nkb = 0 (mod 4).)
+  long nkc = nkb;
+  if constexpr (C::CAUSAL && C::WAVES == 8 && C::SK % 128 == 0)
+    if (f.wave < 4 && nkb == (q0 + BQ - 1) / BK + 1) nkc = nkb - 4;
+  f.run(Q + C::q_off(b), O, b, nkb, nkc);
 }
 
 // Workgroup of C::WAVES waves (64 * C::WAVES threads) over blocks_per_group<C>() query blocks of

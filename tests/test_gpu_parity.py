@@ -199,7 +199,9 @@ def _scale(dtype):
     (2, 256, "f16", False), (2, 256, "f16", True), (3, 384, "bf16", True), (1, 128, "bf16", False),
     (2, 64, "f16", False), (1, 64, "f16", True),
     # one-wave workgroups: a single key block (32 x 32), an odd number of causal query blocks
-    (1, 32, "f16", False), (2, 96, "bf16", True), (3, 160, "f16", False)])
+    (1, 32, "f16", False), (2, 96, "bf16", True), (3, 160, "f16", False),
+    # eight-wave causal blocks, paired per workgroup (waves 0-3 skip the key blocks above the diagonal)
+    (2, 512, "bf16", True), (1, 1024, "f16", True)])
 def test_fused_attention_matches_oracle(heads, seq, dtype, causal):
     say(f"attention {heads} x {seq} x 128 {dtype} causal={causal}")
     prog = W.attention_program(heads, seq, 128, dtype, causal)
@@ -219,6 +221,20 @@ def test_fused_attention_more_keys_than_queries():
     ins = [W.to_dtype(W.normal(40 + i, int(np.prod(s))), "f16").reshape(s) for i, s in enumerate(shapes)]
     exact = exact_attention(*ins, _scale("f16"), False, "f16")
     assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "f16", exact)
+
+
+def test_fused_causal_attention_more_queries_than_keys():
+    """Causal mask with 512 queries and 256 keys: the second 256-query block's keys end before its
+    diagonal, so every wave of it processes every key block (none is skipped as fully masked)."""
+    say("attention causal 2 x 512 queries x 256 keys bf16")
+    specs = [T.spec("bf16", head=2, query=512, dim=128), T.spec("bf16", head=2, key=256, dim=128),
+             T.spec("bf16", head=2, key=256, dim=128)]
+    prog = T.define("cross_causal", specs, W.attention_body("bf16", 128, True))
+    assert _fused(prog)
+    shapes = [(2, 512, 128), (2, 256, 128), (2, 256, 128)]
+    ins = [W.to_dtype(W.normal(50 + i, int(np.prod(s))), "bf16").reshape(s) for i, s in enumerate(shapes)]
+    exact = exact_attention(*ins, _scale("bf16"), True, "bf16")
+    assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16", exact)
 
 
 def test_attention_full_size_on_sampled_heads():

@@ -289,18 +289,23 @@ def _gelu_inputs(dtype, seed, m=512, k=256, n=768):
     return [W.to_dtype(rng.standard_normal((m, k)), dtype), W.to_dtype(rng.standard_normal((k, n)) / 8, dtype)]
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
-def test_epilogue_lookup_table_equals_direct_epilogue(dtype):
+@pytest.mark.parametrize("dtype,shape", [
+    ("bf16", (512, 256, 768)), ("f16", (512, 256, 768)),
+    # 256 x 128 tiles (table read from global memory) and the register-staged kernel (K < 128)
+    ("bf16", (256, 256, 384)), ("bf16", (200, 96, 136))])
+def test_epilogue_lookup_table_equals_direct_epilogue(dtype, shape):
     """A 16-bit contraction whose fused epilogue is a chain of elementwise operations on the contraction
     value and splat constants (here GELU's tanh form, ten operations) runs that chain once per 16-bit
     pattern in a table kernel and looks the result up per element (from LDS in the four-stage 256 x 256
-    contraction). The outputs equal the directly evaluated epilogue (ACCY_GEMM_NO_LUT) bit for bit,
-    and match the oracle."""
+    contraction, from global memory in the other contraction kernels). The outputs equal the directly
+    evaluated epilogue (ACCY_GEMM_NO_LUT) bit for bit, and match the oracle."""
     import os
-    prog = _gelu_contraction(dtype)
+    m, k, n = shape
+    say(f"lookup-table epilogue {dtype} {m} x {k} x {n}")
+    prog = _gelu_contraction(dtype, m, k, n)
     src = hip.plan_source(prog.encode(), compile=False)
     assert "accy_lut_" in src and "f32_to_" in src
-    ins = _gelu_inputs(dtype, 21)
+    ins = _gelu_inputs(dtype, 21, m, k, n)
     table = hip_run(prog, ins)[0]
     os.environ["ACCY_GEMM_NO_LUT"] = "1"
     try:
@@ -310,6 +315,7 @@ def test_epilogue_lookup_table_equals_direct_epilogue(dtype):
         del os.environ["ACCY_GEMM_NO_LUT"]
     assert np.array_equal(np.asarray(table).view(np.uint8), np.asarray(direct).view(np.uint8))
     assert_rowwise(table, oracle_run(prog, ins)[0], 2e-2, dtype)
+
 
 def test_lookup_table_kernel_runs_once_per_executor():
     """The table kernel's output depends on constants only: an executor runs it on its first
@@ -339,6 +345,7 @@ def test_lookup_table_kernel_runs_once_per_executor():
     finally:
         s.release(h)
         stream.destroy()
+
 
 def test_decoder_with_fused_causal_attention():
     say("decoder 1 x 128 x 256, 2 heads x 128, ffn 512, bf16")

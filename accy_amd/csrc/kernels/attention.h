@@ -248,8 +248,29 @@ struct Worker {
   float m, l;      // subtracted maximum (log2 domain, finite) and this lane's half of the row sum
   long q0;
   int wave, lane;
+  // The workgroup's next query block (blocks run back to back): once every wave has read the last
+  // K stage of this block, its Q^T and its first two K tiles are issued (ready: this block's were).
+  const u16_t* next_q = nullptr;  // Q of the batch index, or nullptr when no block follows
+  long next_q0 = 0, next_nkb = 0;
+  bool ready = false;
 
   __device__ __forceinline__ long query() const { return q0 + 32 * wave + (lane & 31); }
+
+  // Q^T of the queries q0 + 32 wave + (lane & 31) (this wave's 32 queries) into registers.
+  __device__ __forceinline__ void load_q(const u16_t* __restrict__ qp, long first) {
+    const long q = first + 32 * wave + (lane & 31);
+#pragma unroll
+    for (int dd = 0; dd < DS; ++dd) qf[dd] = *(const u32x4*)(qp + q * C::Q_S + 16 * dd + 8 * (lane >> 5));
+  }
+
+  // Called after the workgroup's last meeting at or after step nkb: no wave reads K any more, so
+  // the next block's Q^T (into qf, free since the last score MFMA) and K(0), K(1) can be issued.
+  __device__ __forceinline__ void issue_next() {
+    if (next_q == nullptr) return;
+    load_q(next_q, next_q0);
+    dma_share<PER>(kb, 0, off.kg, sh.ks[0], wave);
+    if (next_nkb > 1) dma_share<PER>(kb, BK * C::K_S, off.kg, sh.ks[1], wave);
+  }
 
   // Scores of keys above the query are -inf (blocks that cross the diagonal only). Register r holds
   // key k0 + 8 (r / 4) + 4 (lane / 32) + r % 4, so the test is one 32-bit compare of a constant
@@ -382,28 +403,31 @@ struct Worker {
   // blocks that are masked for every query of this wave) only meet the workgroup and issue loads.
   __device__ __forceinline__ void run(const u16_t* __restrict__ qp, u16_t* __restrict__ out, long b, long nkb,
                                       long nkc) {
-#pragma unroll
-    for (int dd = 0; dd < DS; ++dd) qf[dd] = *(const u32x4*)(qp + query() * C::Q_S + 16 * dd + 8 * (lane >> 5));
+    if (!ready) {
+      load_q(qp, q0);
+      off.init(wave, lane);
+      dma_share<PER>(kb, 0, off.kg, sh.ks[0], wave);
+      if (nkb > 1) dma_share<PER>(kb, BK * C::K_S, off.kg, sh.ks[1], wave);
+    }
 #pragma unroll
     for (int dt = 0; dt < DTN; ++dt) o[dt] = f32x16{};
     m = -0x1.fffffep127f;
     l = 0.0f;
     alpha[0] = alpha[1] = 1.0f;
-    off.init(wave, lane);
-    dma_share<PER>(kb, 0, off.kg, sh.ks[0], wave);
-    if (nkb > 1) dma_share<PER>(kb, BK * C::K_S, off.kg, sh.ks[1], wave);
     step0(nkb);
     if (nkb == 1) {
       step<1, false, true, false>(1, nkb);
       step<2, false, false, true>(2, nkb);
+      issue_next();
     } else {
       steps(nkb, nkc);
     }
     epilogue(out, b);
     if (nkc < nkb) {
-      // nkc = 0 (mod 4): the remaining even steps are nkc + 2 and nkc + 4
+      // nkc = 0 (mod 4): the remaining even steps are nkc + 2 and nkc + 4 (= nkb, the last meeting)
       meet<2>(nkc + 2, nkb);
       meet<0>(nkc + 4, nkb);
+      issue_next();
     }
   }
 
@@ -423,17 +447,23 @@ struct Worker {
     constexpr long BQ = 32 * WAVES, NKB = C::SK / BK;
     constexpr int MOD = !C::CAUSAL ? (int)((NKB - 2) % 4) : (BQ % 128 == 0 && C::SK % 128 == 0 ? 2 : -1);
     const long r = MOD >= 0 ? MOD : nkc - t;
+    // The next block's loads follow the first meeting at or after step nkc (the last one of this
+    // block when nkc == nkb).
+    const bool last = nkc == nkb;
     if (r == 0) {
       step<2, false, true, true>(t, nkb);
+      if (last) issue_next();
       step<3, false, false, true>(t + 1, nkb);
     } else if (r == 1) {
       step<2, true, true, true>(t, nkb);
       step<3, false, true, true>(t + 1, nkb);
       step<0, false, false, true>(t + 2, nkb);
+      if (last) issue_next();
     } else if (r == 2) {
       step<2, true, true, true>(t, nkb);
       step<3, true, true, true>(t + 1, nkb);
       step<0, false, true, true>(t + 2, nkb);
+      if (last) issue_next();
       step<1, false, false, true>(t + 3, nkb);
     } else {
       step<2, true, true, true>(t, nkb);
@@ -441,6 +471,7 @@ struct Worker {
       step<0, true, true, true>(t + 2, nkb);
       step<1, false, true, true>(t + 3, nkb);
       step<2, false, false, true>(t + 4, nkb);
+      if (last) issue_next();
     }
   }
 
@@ -481,34 +512,39 @@ struct Worker {
   }
 };
 
-// Query blocks per workgroup: under a causal mask with an even number of query blocks, a workgroup
+// Query blocks per workgroup. Under a causal mask with an even number of query blocks, a workgroup
 // takes block NQB - 1 - p and then block p, so that every workgroup streams the same number of key
-// blocks (the heavy blocks start first); the grid is NB * NQB / blocks_per_group workgroups.
+// blocks (the heavy blocks start first). Without a mask, pairs of blocks when that leaves a whole
+// number of rounds of 256 workgroups (one per CU of an MI355X): the second block's Q^T and first K
+// tiles load during the first block's last steps instead of after a workgroup launch. The grid is
+// NB * NQB / blocks_per_group workgroups.
 template <class C>
 constexpr long blocks_per_group() {
   constexpr long NQB = C::SQ / (32 * C::WAVES);
-  return C::CAUSAL && NQB % 2 == 0 ? 2 : 1;
+  if constexpr (C::CAUSAL) return NQB % 2 == 0 ? 2 : 1;
+  return NQB % 2 == 0 && (C::NB * NQB) % 512 == 0 ? 2 : 1;
 }
 
-// One query block (queries qb * 32 * WAVES ...) of batch index b. Every wave meets the same
-// barriers, so blocks can follow each other.
+// Key blocks a query block starting at q0 reads (under the causal mask, up to its last query).
 template <class C>
-__device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __restrict__ Q, const u16_t* __restrict__ K,
-                                            const u16_t* __restrict__ V, u16_t* __restrict__ O, long b, long qb) {
+__device__ __forceinline__ long key_blocks(long q0) {
   constexpr long BQ = 32 * C::WAVES, NKB = C::SK / BK;
-  const long q0 = qb * BQ;
   long nkb = NKB;
   if constexpr (C::CAUSAL) {
     const long last = (q0 + BQ - 1) / BK + 1;
     nkb = last < nkb ? last : nkb;
   }
-  Worker<C> f;
-  f.sh = sh;
-  f.kb = K + C::k_off(b);
-  f.vb = V + C::v_off(b);
+  return nkb;
+}
+
+// One query block (queries qb * 32 * WAVES ...) of batch index b on worker f (Qb: the batch index's
+// Q). Every wave meets the same barriers, so blocks can follow each other.
+template <class C>
+__device__ __forceinline__ void flash_block(Worker<C>& f, const u16_t* __restrict__ Qb, u16_t* __restrict__ O, long b,
+                                            long qb) {
+  constexpr long BQ = 32 * C::WAVES;
+  const long q0 = qb * BQ, nkb = key_blocks<C>(q0);
   f.q0 = q0;
-  f.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  f.lane = (int)(threadIdx.x & 63);
   // Under the causal mask the last four key blocks of a 256-query block lie above the diagonal for
   // every query of waves 0-3 (queries q0 .. q0 + 127) when the block's keys reach its last query:
   // those waves skip their work and only meet the workgroup there. With waves w and w + 4 on one
@@ -517,7 +553,7 @@ __device__ __forceinline__ void flash_block(const Lds<C>& sh, const u16_t* __res
   long nkc = nkb;
   if constexpr (C::CAUSAL && C::WAVES == 8 && C::SK % 128 == 0)
     if (f.wave < 4 && nkb == (q0 + BQ - 1) / BK + 1) nkc = nkb - 4;
-  f.run(Q + C::q_off(b), O, b, nkb, nkc);
+  f.run(Qb, O, b, nkb, nkc);
 }
 
 // Workgroup of C::WAVES waves (64 * C::WAVES threads) over blocks_per_group<C>() query blocks of
@@ -533,7 +569,6 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
   u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
   u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
-  const Lds<C> sh{ks, vs};
 
   // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
   // query blocks with the most keys start first.
@@ -542,15 +577,25 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
   const long b = t / PER_B, p = t % PER_B;
   if (b >= C::NB) return;  // a grid larger than the work
+  Worker<C> f;
+  f.sh = Lds<C>{ks, vs};
+  f.kb = K + C::k_off(b);
+  f.vb = V + C::v_off(b);
+  f.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  f.lane = (int)(threadIdx.x & 63);
+  const u16_t* __restrict__ Qb = Q + C::q_off(b);
   if constexpr (PAIR == 2) {
-    // one copy of the block code, run twice
+    // one copy of the block code, run twice; the first issues the second's first loads
 #pragma unroll 1
     for (int i = 0; i < 2; ++i) {
-      flash_block<C>(sh, Q, K, V, O, b, i == 0 ? NQB - 1 - p : p);
-      gemm::wait_vmcnt<0>();  // the block's output stores, before the next block's waits
+      f.next_q = i == 0 ? Qb : nullptr;
+      f.next_q0 = p * BQ;
+      f.next_nkb = key_blocks<C>(p * BQ);
+      f.ready = i == 1;
+      flash_block<C>(f, Qb, O, b, i == 0 ? NQB - 1 - p : p);
     }
   } else {
-    flash_block<C>(sh, Q, K, V, O, b, C::CAUSAL ? NQB - 1 - p : p);
+    flash_block<C>(f, Qb, O, b, C::CAUSAL ? NQB - 1 - p : p);
   }
 }
 

@@ -282,10 +282,11 @@ void Planner::attention(uint32_t pv, const Attn& at, const AttnLayout& L) {
   KernelStep ks;
   ks.source = src.str();
   ks.name = nm;
-  // Causal with an even number of query blocks: two complementary blocks per workgroup
-  // (attn::blocks_per_group), so every workgroup streams the same number of keys.
+  // Two query blocks per workgroup (attn::blocks_per_group, the same rule): causal with an even
+  // number of query blocks (complementary blocks, so every workgroup streams the same number of
+  // keys), or unmasked when the pairs still fill whole rounds of 256 workgroups.
   const int64_t nqb = L.sq / (32 * waves);
-  const int64_t pair = at.causal && nqb % 2 == 0 ? 2 : 1;
+  const int64_t pair = nqb % 2 == 0 && (at.causal || (L.nb * nqb) % 512 == 0) ? 2 : 1;
   ks.grid[0] = (uint32_t)(L.nb * nqb / pair);
   ks.block[0] = 64 * waves;  // one wave per 32 queries
   ks.klass = "attention";

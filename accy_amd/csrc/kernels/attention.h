@@ -18,8 +18,12 @@
 // Softmax: f32 throughout, online over key blocks in the log2 domain: e = exp2(s * scale * log2 e -
 // m) with v_exp_f32. The subtracted maximum m only moves when the running maximum exceeds it by more
 // than 8 (a factor 256), so the accumulators are rescaled rarely; e <= 256 stays well inside the
-// 16-bit range of the P operand. Row sums accumulate the f32 e; the result is O / sum.
+// 16-bit range of the P operand. Row sums accumulate the 16-bit rounded e that the P.V product
+// consumes (a dot product of each packed pair with ones), so numerator and denominator weight every
+// key alike; the result is O / sum.
 //
+// A workgroup runs one or two query blocks (blocks_per_group); with two, the first issues the
+// second's first loads after its last barrier.
 // K and V tiles go straight from global memory to LDS (global_load_lds_dwordx4), four stages per
 // operand in distinct LDS arrays so that the compiler's wait analysis can tell the in-flight loads
 // from the reads. Layouts (256-byte rows of 128 elements, conflict-free reads):

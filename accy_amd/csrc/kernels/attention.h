@@ -24,6 +24,7 @@
 //
 // A workgroup runs one or two query blocks (blocks_per_group); with two, the first issues the
 // second's first loads after its last barrier.
+//
 // K and V tiles go straight from global memory to LDS (global_load_lds_dwordx4), four stages per
 // operand in distinct LDS arrays so that the compiler's wait analysis can tell the in-flight loads
 // from the reads. Layouts (256-byte rows of 128 elements, conflict-free reads):

@@ -237,6 +237,28 @@ def test_fused_causal_attention_more_queries_than_keys():
     assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16", exact)
 
 
+def test_fused_attention_paired_blocks_without_mask():
+    """Without a mask, a workgroup takes two query blocks when the pairs fill whole rounds of 256
+    workgroups (here 256 heads x 2 blocks of 256 queries); the first block issues the second's Q^T
+    and first K tiles. Every head against float64, two heads against the oracle."""
+    say("attention f16 256 x 512 x 512 x 128 (paired blocks)")
+    heads, seq = 256, 512
+    prog = W.attention_program(heads, seq, 128, "f16")
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "accy::attn::flash<" in src and "WAVES = 8" in src
+    q, k, v = W.attention_inputs(heads, seq, 128, "f16", seed=77)
+    got = hip_run(prog, [q, k, v])[0]
+    sel = [0, heads - 1]
+    sub = [q[sel], k[sel], v[sel]]
+    ref = oracle_run(W.attention_program(2, seq, 128, "f16"), sub)[0]
+    assert_attention(got[sel], ref, 2e-2, "f16", exact_attention(*sub, _scale("f16"), False, "f16"))
+    exact = exact_attention(q, k, v, _scale("f16"), False, "f16")
+    g = to_f32(np.asarray(got), "f16").astype(np.float64)
+    # every head: within 2e-2 of the float64 formula relative to its largest output
+    err = np.abs(g - exact).max(axis=(1, 2)) / np.abs(exact).max(axis=(1, 2))
+    assert err.max() <= 2e-2, f"worst head {int(err.argmax())}: {err.max():.3e}"
+
+
 def test_attention_full_size_on_sampled_heads():
     say("attention f16 32 x 4096 x 4096 x 128 (full)")
     q, k, v = W.attention_inputs(32, 4096, 128, "f16")
@@ -502,7 +524,8 @@ def test_fused_16bit_attention_head_dim_64(heads, seq, dtype, causal):
                      exact_attention(*ins, scale, causal, dtype))
 
 
-@pytest.mark.parametrize("heads,seq,dtype,causal", [(2, 256, "f16", False), (2, 384, "bf16", True), (1, 96, "bf16", False)])
+@pytest.mark.parametrize("heads,seq,dtype,causal", [(2, 256, "f16", False), (2, 384, "bf16", True), (1, 96, "bf16", False),
+                                                    (2, 512, "bf16", True)])  # paired four-wave blocks
 def test_fused_16bit_attention_head_dim_256(heads, seq, dtype, causal):
     """Head dimension 256: one wave per SIMD (four-wave workgroups, 128 KiB of K / V stages)."""
     say(f"{dtype} attention {heads} x {seq} x 256 causal={causal}")

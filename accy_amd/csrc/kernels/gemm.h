@@ -635,11 +635,18 @@ __device__ __forceinline__ void mma16_dma_tile(const u16_t* __restrict__ A, cons
   }
 }
 
+// Tile rows per group of the tile walk (C::GROUP_M when the configuration sets it, else 8). With 32
+// workgroups per XCD at a time, 8 gives each XCD 8 A row panels x 4 B column panels and 4 gives 4 x 8:
+// the same panel count, but with 4 each A panel of an 8-panel-wide B is read by one XCD only, which
+// the planner prefers when A is the larger operand (its repeated reads would come from HBM).
+template <class C, class = void> struct GroupM { static constexpr int value = 8; };
+template <class C> struct GroupM<C, decltype((void)C::GROUP_M)> { static constexpr int value = C::GROUP_M; };
+
 template <class C, class Epi>
 __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16_t* __restrict__ B, const Epi& epi) {
   constexpr long TILES_M = (C::M + C::BM - 1) / C::BM, TILES_N = (C::N + C::BN - 1) / C::BN;
   long tm, tn;
-  tile_of<TILES_M, TILES_N, 8>((long)blockIdx.x, tm, tn);
+  tile_of<TILES_M, TILES_N, GroupM<C>::value>((long)blockIdx.x, tm, tn);
   mma16_dma_tile<C>(A, B, epi, tm, tn);
 }
 

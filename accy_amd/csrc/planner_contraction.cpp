@@ -582,8 +582,15 @@ void Planner::gemm(uint32_t v, const GemmShape& gs, const OutStrides& os) {
     }
     const bool placeholder = n_tiles.size() > 1;
     if (dma) {
+      // Tile walk: groups of 4 tile rows when A is the larger operand (each XCD then reads each of
+      // its A panels once per round where B is at least 8 tiles wide), else 8 (gemm::GroupM).
+      int group_m = gs.m > gs.n ? 4 : 8;
+      if (const char* e = std::getenv("ACCY_GEMM_GROUP_M")) {
+        const int g = std::atoi(e);
+        if (g == 1 || g == 2 || g == 4 || g == 8 || g == 16) group_m = g;
+      }
       src << "  static constexpr int BM = " << dm << ", BN = " << (placeholder ? "ACCY_N_TILE" : std::to_string(dn))
-          << ", STAGES = 4;\n};\n";
+          << ", STAGES = 4, GROUP_M = " << group_m << ";\n};\n";
     } else {
       src << "  static constexpr int BM = " << BM << ", BN = " << BN << ", BK = " << BK << ", WAVES_M = " << WM
           << ", WAVES_N = " << WN << ";\n};\n";

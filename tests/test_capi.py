@@ -80,6 +80,19 @@ def test_decoder_gelu_epilogue_is_a_lookup_table():
     assert src.count("accy_lut_") == 1 and "// lut:%" in src
     assert src.count("[accy::f32_to_bf16(v)]") == 1
 
+
+def test_contraction_tile_walk_follows_the_larger_operand():
+    """The direct-to-LDS contraction walks its tiles in groups of 4 tile rows when A is the larger
+    operand (M > N: each XCD reads each A panel once per round where B is at least 8 tiles wide) and
+    of 8 otherwise."""
+    def cfg(m, k, n):
+        src = hip.plan_source(W.gemm_program(m, k, n, "bf16", "contract"), compile=False)
+        return [line for line in src.split("\n") if "STAGES = 4" in line][0]
+    assert "GROUP_M = 4" in cfg(8192, 512, 2048)
+    assert "GROUP_M = 8" in cfg(2048, 512, 8192)
+    assert "GROUP_M = 8" in cfg(4096, 512, 4096)
+
+
 def test_attention_fusion_keeps_values_read_elsewhere():
     # the probabilities are also an output, so they must be materialised: no fusion
     def body(b, a):

@@ -95,14 +95,14 @@ def test_contraction_follows_the_imported_n_tile():
     src = hip.plan_source(prog)
     (key, cand, count), = tuning_lines(src)
     assert key.startswith("gfx950/gemm/") and (cand, count) == ("0", "2")
-    assert "BN = 256, STAGES = 4;" in src and "grid 1024 " in src
+    assert "BN = 256, STAGES = 4," in src and "grid 1024 " in src
     hip.tuning_import(artifact([(key, 2, 1, 10, 3)]))
     src = hip.plan_source(prog, compile=True)   # the selected candidate builds for gfx950
-    assert "BN = 128, STAGES = 4;" in src and "grid 2048 " in src
+    assert "BN = 128, STAGES = 4," in src and "grid 2048 " in src
     # A record for another key (or candidate count) changes nothing.
     hip.tuning_clear()
     hip.tuning_import(artifact([(key + "x", 2, 1, 10, 3), (key, 3, 1, 10, 3)]))
-    assert "BN = 256, STAGES = 4;" in hip.plan_source(prog)
+    assert "BN = 256, STAGES = 4," in hip.plan_source(prog)
 
 
 def test_which_config_kernels_are_tunable():

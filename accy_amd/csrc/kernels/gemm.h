@@ -661,7 +661,7 @@ __device__ __forceinline__ void mma16_dma_group(const u16_t* __restrict__ A, con
   const long bid = xcd_contiguous<G * TILES_M * TILES_N>((long)blockIdx.x);
   const int g = (int)(bid % G);
   long tm, tn;
-  tile_in_groups<TILES_M, TILES_N, 8>(bid / G, tm, tn);
+  tile_in_groups<TILES_M, TILES_N, GroupM<C>::value>(bid / G, tm, tn);
   const u16_t* __restrict__ Bg = B[0];
 #pragma unroll
   for (int i = 1; i < G; ++i)

@@ -130,8 +130,11 @@ __device__ __forceinline__ float sincos_core(float r, int q) {
 
 // sin with one polynomial: x = k pi + r, k = rint(x / pi) read off the low mantissa bits of
 // x / pi + 1.5 * 2^23 (so the sign (-1)^k needs no integer conversion, and k = +0 for x = -0),
-// r = x - k pi by the three-part reduction with FMAs, then the odd Taylor polynomial of sin through
-// r^13 on [-pi/2, pi/2] (truncation below 7e-10) and the sign.
+// r = x - k pi by the three-part reduction with FMAs, then an odd polynomial through r^9 and the
+// sign. The polynomial r + r^3 P(r^2), P of degree 3, minimises the largest relative error against
+// sin on [-pi/2, pi/2] (Remez exchange on (sin r - r) / r^3 weighted by r^3 / sin r; 6.1e-9 before
+// the coefficients are rounded to f32), two FMAs fewer than the Taylor polynomial through r^13 with
+// the same accuracy in f32 (1.74 against 1.80 ulp worst case over 4.6 million arguments).
 // The library's reductions for |x| >= 2^17, out of line so that their code does not sit between the
 // loads and arithmetic of every element that takes the fast path (`const`: no memory effects, so
 // loads still move and merge across the calls).
@@ -149,11 +152,9 @@ __device__ __forceinline__ float sin_f32(float x) {
   r = __builtin_fmaf(-k, P2, r);
   r = __builtin_fmaf(-k, P3, r);
   const float r2 = r * r;
-  float p = __builtin_fmaf(r2, 0x1.612462p-33f, -0x1.ae6456p-26f);  // 1/13!, -1/11!
-  p = __builtin_fmaf(r2, p, 0x1.71de3ap-19f);                        // 1/9!
-  p = __builtin_fmaf(r2, p, -0x1.a01a02p-13f);                       // -1/7!
-  p = __builtin_fmaf(r2, p, 0x1.111112p-7f);                         // 1/5!
-  p = __builtin_fmaf(r2, p, -0x1.555556p-3f);                        // -1/3!
+  float p = __builtin_fmaf(r2, 0x1.5dbdf0p-19f, -0x1.9f6ffep-13f);
+  p = __builtin_fmaf(r2, p, 0x1.110ed4p-7f);
+  p = __builtin_fmaf(r2, p, -0x1.55554cp-3f);
   // sin r has the sign of r on [-pi/2, pi/2]; or-ing r's sign bit in only matters for r = -0 (the
   // FMA turns it into +0).
   const float s = __builtin_fmaf(r * r2, p, r);

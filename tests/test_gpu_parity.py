@@ -237,22 +237,24 @@ def test_fused_causal_attention_more_queries_than_keys():
     assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16", exact)
 
 
-def test_fused_attention_paired_blocks_without_mask():
+@pytest.mark.parametrize("heads,seq,hd,waves", [(256, 512, 128, 8), (128, 512, 256, 4)])
+def test_fused_attention_paired_blocks_without_mask(heads, seq, hd, waves):
     """Without a mask, a workgroup takes two query blocks when the pairs fill whole rounds of 256
-    workgroups (here 256 heads x 2 blocks of 256 queries); the first block issues the second's Q^T
-    and first K tiles. Every head against float64, two heads against the oracle."""
-    say("attention f16 256 x 512 x 512 x 128 (paired blocks)")
-    heads, seq = 256, 512
-    prog = W.attention_program(heads, seq, 128, "f16")
+    workgroups (256 heads x 2 blocks of 256 queries; 128 heads x 4 blocks of 128 queries at head
+    dimension 256); the first block issues the second's Q^T and first K tiles. Every head against
+    float64, two heads against the oracle."""
+    say(f"attention f16 {heads} x {seq} x {seq} x {hd} (paired blocks)")
+    prog = W.attention_program(heads, seq, hd, "f16")
     src = hip.plan_source(prog.encode(), compile=False)
-    assert "accy::attn::flash<" in src and "WAVES = 8" in src
-    q, k, v = W.attention_inputs(heads, seq, 128, "f16", seed=77)
+    assert "accy::attn::flash<" in src and f"WAVES = {waves}" in src
+    q, k, v = W.attention_inputs(heads, seq, hd, "f16", seed=77)
     got = hip_run(prog, [q, k, v])[0]
     sel = [0, heads - 1]
     sub = [q[sel], k[sel], v[sel]]
-    ref = oracle_run(W.attention_program(2, seq, 128, "f16"), sub)[0]
-    assert_attention(got[sel], ref, 2e-2, "f16", exact_attention(*sub, _scale("f16"), False, "f16"))
-    exact = exact_attention(q, k, v, _scale("f16"), False, "f16")
+    scale = float(to_f32(W.to_dtype(np.array([1 / math.sqrt(hd)]), "f16"), "f16")[0])
+    ref = oracle_run(W.attention_program(2, seq, hd, "f16"), sub)[0]
+    assert_attention(got[sel], ref, 2e-2, "f16", exact_attention(*sub, scale, False, "f16"))
+    exact = exact_attention(q, k, v, scale, False, "f16")
     g = to_f32(np.asarray(got), "f16").astype(np.float64)
     # every head: within 2e-2 of the float64 formula relative to its largest output
     err = np.abs(g - exact).max(axis=(1, 2)) / np.abs(exact).max(axis=(1, 2))

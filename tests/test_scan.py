@@ -174,3 +174,41 @@ def test_scan_program_invoked_repeatedly_reuses_its_carry_buffers():
             p.launch(inputs, got)
             assert np.array_equal(got[0], ref[0])
             assert_rel(got[1], ref[1], 1e-5)
+
+
+# ---- long scans ----
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["relax", "power", "count"])
+def test_long_scans_invoked_repeatedly(case):
+    """Loops of 70-100 iterations against the oracle, the same executor invoked three times with
+    another program's work and a synchronisation between the invocations; every invocation equals
+    the first bit for bit."""
+    if case == "relax":
+        prog, inputs = two_carries(100), _relax_inputs(seed=21)
+    elif case == "power":
+        prog, inputs = power(40), _power_inputs(seed=22)
+        inputs[1] = inputs[1] * np.float32(0.9)  # keep A B^40 finite
+    else:
+        i, n, f = np.arange(100, dtype=np.int32), np.array(7, np.int32), np.ones(8, np.float32)
+        prog, inputs = integer_counter(70), [i, n, f]
+    ref = oracle_run(prog, inputs)
+    other = doubling(3)
+    x = np.linspace(-1, 1, 1000).astype(np.float32)
+    first = None
+    with hip.Hip(prog) as p:
+        for _ in range(3):
+            got = out_arrays(prog)
+            p.launch(inputs, got)
+            if first is None:
+                first = [np.array(g, copy=True) for g in got]
+            for g, e in zip(got, first):
+                assert np.array_equal(np.asarray(g).reshape(-1).view(np.uint8), np.asarray(e).reshape(-1).view(np.uint8))
+            hip_run(other, [x])  # other work between the invocations
+    if case == "relax":
+        assert np.array_equal(got[0], ref[0])
+        assert_rel(got[1], ref[1], 1e-5)
+    elif case == "power":
+        assert_normwise(got[0], ref[0], 1e-4)
+    else:
+        assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])

@@ -151,6 +151,14 @@ int accy_hip_compile(const uint8_t* wire_bytes, size_t wire_len, accy_hip_handle
       return fail_with(ACCY_HIP_COMPILE_FAILED, e.what());
     }
     auto exec = std::make_shared<Executor>(std::move(prog), std::move(plan));
+    // The allocation-free entry point's device scratch: its address on this device is looked up now
+    // (which may load the array's code object), so that accy_hip_invoke_device_scratch, possibly under
+    // graph capture, only reads the kept address. A failure here is reported by that call.
+    {
+      void* base = nullptr;
+      const char* why = "";
+      (void)scratch_region(&base, &why);
+    }
     std::lock_guard<std::mutex> lock(g_mu);
     Entry* e = &g_entries[index];
     if (e->live) {  // taken by another thread meanwhile

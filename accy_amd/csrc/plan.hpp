@@ -45,8 +45,8 @@ struct KernelStep {
   std::string tuning_key;
   uint32_t candidate_count = 1;
   uint32_t candidate = 0;
-  // The kernel's output depends on constants only (a lookup table): it runs on an executor's first
-  // invocation, whose temporaries persist, and on every scratch-bound one.
+  // The kernel's output depends on constants only (a lookup table): an executor runs it once, when it
+  // is built, into its own temporaries (which persist); a scratch-bound invocation runs it every time.
   bool once = false;
 };
 

@@ -182,6 +182,24 @@ Executor::Executor(Program program, Plan plan) : program_(std::move(program)), p
       t.algorithmic_flops = st.kernel.algorithmic_flops;
       timings_.push_back(t);
     }
+    // Run-once kernels (lookup tables) depend on constants only: they fill their temporaries here, on
+    // the executor's stream, before any invocation can be enqueued or captured into a graph, so every
+    // later invocation on any stream finds the tables complete.
+    for (size_t i = 0; i < plan_.slots.size(); ++i)
+      if (plan_.slots[i].role == SlotInfo::Const || plan_.slots[i].role == SlotInfo::Temp) bound_[i] = owned_[i];
+    bool any_once = false;
+    for (size_t i = 0; i < plan_.steps.size(); ++i) {
+      const Step& st = plan_.steps[i];
+      if (st.type != Step::Kernel || !st.kernel.once) continue;
+      for (int a : st.kernel.args) {
+        const SlotInfo::Role r = plan_.slots[(size_t)a].role;
+        if (r != SlotInfo::Const && r != SlotInfo::Temp)
+          throw HipFailure(kStatusCompileFailed, st.kernel.label + ": a run-once kernel reads or writes a caller buffer");
+      }
+      launch(i, stream_);
+      any_once = true;
+    }
+    if (any_once) check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
   } catch (...) {
     for (void* p : owned_)
       if (p) (void)hipFree(p);
@@ -270,6 +288,19 @@ const std::vector<KernelTiming>& Executor::timings() {
   return timings_;
 }
 
+void Executor::launch(size_t step, hipStream_t stream) {
+  const KernelStep& k = plan_.steps[step].kernel;
+  std::vector<void*> ptrs(k.args.size());
+  std::vector<void*> params(k.args.size());
+  for (size_t a = 0; a < k.args.size(); ++a) {
+    ptrs[a] = bound_[(size_t)k.args[a]];
+    params[a] = &ptrs[a];
+  }
+  check(hipModuleLaunchKernel(fn_[step], k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2],
+                              k.shared_bytes, stream, params.data(), nullptr),
+        "hipModuleLaunchKernel");
+}
+
 void Executor::run_steps(hipStream_t stream, uint8_t* scratch) {
   for (size_t i = 0; i < plan_.slots.size(); ++i) {
     if (plan_.slots[i].role == SlotInfo::Const) bound_[i] = owned_[i];
@@ -304,30 +335,18 @@ void Executor::run_steps(hipStream_t stream, uint8_t* scratch) {
       continue;
     }
     const KernelStep& k = st.kernel;
-    if (k.once && !scratch) {
-      if (once_done_.size() != plan_.steps.size()) once_done_.assign(plan_.steps.size(), false);
-      if (once_done_[i]) {
-        if (ev) {
-          check(hipEventRecord(ev[2 * ki], stream), "hipEventRecord");
-          check(hipEventRecord(ev[2 * ki + 1], stream), "hipEventRecord");
-          skipped[ki] = 1;
-        }
-        ++ki;
-        continue;
+    if (k.once && !scratch) {  // filled by the constructor; the executor's own temporaries persist
+      if (ev) {
+        check(hipEventRecord(ev[2 * ki], stream), "hipEventRecord");
+        check(hipEventRecord(ev[2 * ki + 1], stream), "hipEventRecord");
+        skipped[ki] = 1;
       }
+      ++ki;
+      continue;
     }
     if (skipped) skipped[ki] = 0;
-    std::vector<void*> ptrs(k.args.size());
-    std::vector<void*> params(k.args.size());
-    for (size_t a = 0; a < k.args.size(); ++a) {
-      ptrs[a] = bound_[(size_t)k.args[a]];
-      params[a] = &ptrs[a];
-    }
     if (ev) check(hipEventRecord(ev[2 * ki], stream), "hipEventRecord");
-    check(hipModuleLaunchKernel(fn_[i], k.grid[0], k.grid[1], k.grid[2], k.block[0], k.block[1], k.block[2],
-                                k.shared_bytes, stream, params.data(), nullptr),
-          "hipModuleLaunchKernel");
-    if (k.once && !scratch) once_done_[i] = true;
+    launch(i, stream);
     if (ev) check(hipEventRecord(ev[2 * ki + 1], stream), "hipEventRecord");
     ++ki;
   }

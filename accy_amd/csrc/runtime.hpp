@@ -83,12 +83,12 @@ class Executor {
 
  private:
   void run_steps(hipStream_t stream, uint8_t* scratch);
+  void launch(size_t step, hipStream_t stream);  // one kernel step with the slots bound now
   Program program_;
   Plan plan_;
   std::vector<void*> owned_;     // device allocation per slot (Temp / Const; staging for Input / Output)
   std::vector<void*> bound_;     // pointer used for each slot during a run
   std::vector<hipFunction_t> fn_;
-  std::vector<bool> once_done_;    // per step: a run-once kernel has run (KernelStep::once)
   std::vector<uint8_t> skipped_;   // per profiled call and kernel: a run-once kernel was skipped
   hipStream_t stream_ = nullptr;
   bool profiling_ = false;

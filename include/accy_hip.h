@@ -109,8 +109,10 @@ int accy_hip_invoke_device(accy_hip_handle h, const void* const* inputs, size_t 
  * graph capture, tight serving loops, harnesses that forbid hipMalloc): accy_hip_invoke_device with
  * every intermediate buffer of the run (temporaries between kernels, chunked-fold partials, scan
  * carries) placed in one static device array of 512 MiB that each GPU the library runs on holds until
- * the process ends, instead of the program's own allocations. It calls no hipMalloc / hipFree and
- * records no profiling events. A program whose intermediates need more than 512 MiB returns
+ * the process ends. The call itself calls no hipMalloc / hipFree and records no profiling events;
+ * accy_hip_compile, which the caller runs beforehand, still allocates the executor's own buffers
+ * (constants, and the intermediates that accy_hip_invoke_device uses) and looks up the array's address
+ * on the current device. A program whose intermediates need more than 512 MiB returns
  * ACCY_HIP_OUT_OF_MEMORY before anything is launched. Every call on one GPU uses the same array and
  * leaves the last call's contents in it (each kernel writes an intermediate in full before it is
  * read, so nothing needs clearing): calls that overlap on one GPU, on any streams, race. */

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import ctypes
+import os
 import sys
 from pathlib import Path
 
@@ -13,7 +14,9 @@ sys.path.insert(0, str(ROOT))
 
 from accy_amd import tensor as T  # noqa: E402
 
-ORACLE_LIB = ROOT / "oracle" / "build" / "liboracle.so"
+# ACCY_ORACLE_LIB names another build of the oracle (a copy with a mistake planted on purpose, to
+# show that the pinning tests catch it).
+ORACLE_LIB = Path(os.environ.get("ACCY_ORACLE_LIB", ROOT / "oracle" / "build" / "liboracle.so"))
 
 
 def pytest_configure(config):

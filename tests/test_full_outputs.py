@@ -10,10 +10,11 @@ the whole output, so that a wrong tile number, batch or head offset anywhere in 
 * C3 contraction (the benchmarked mul + sum spelling), f32 and bf16: every element of C against the
   float64 product A B: normwise within BASELINE's 1e-3 (f32) / 2e-2 (bf16), and per element within
   the forward error bound of an f32 sum of K products in any order, K u sum_k |a_ik b_kj| (plus the
-  truncating bf16 store, under 2^-7 relative). A single-tile fault is about 30x that bound.
-* C4 attention: every head, on 64 fixed query rows per head, against float64 softmax(scale q k^T) v
-  from the same f16 inputs: within 2e-3 normwise per head (measured about 5e-4; runCpu's own per-op
-  f16 evaluation is about 1.7e-3 away).
+  truncating bf16 store, under 2^-7 relative). A single-tile fault is about 30x that bound. For
+  bf16, 16 rows also against runCpu's plan of this spelling (per-product bf16 truncation) at 2e-2.
+* C4 attention: every query row of every head against float64 softmax(scale q k^T) v from the same
+  f16 inputs: each row within 2e-3 of its largest magnitude (measured about 5e-4 normwise; runCpu's
+  own per-op f16 evaluation is about 1.7e-3 away).
 * C5 decoder block: all four batch elements against a float64 formulation of the block (RMSNorm,
   projections, causal softmax attention, GELU with the tanh approximation, residuals) from the same
   bf16 inputs: each batch element no further from it than 1.5x runCpu's own error on batch element 2
@@ -25,7 +26,8 @@ import numpy as np
 import pytest
 
 from accy_amd import workloads as W
-from conftest import assert_rel, hip_run, oracle_run, to_f32
+from conftest import assert_no_less_accurate, assert_normwise, assert_rel, hip_run, oracle_run, to_f32
+from test_cpu_plan import lib as plan_lib
 
 pytestmark = pytest.mark.gpu
 
@@ -76,21 +78,41 @@ def test_c3_contraction_every_element(dtype, tol):
         bound = 2.0 ** -7 * np.abs(exact) + (1 + 2.0 ** -7) * bound
     bad = err > bound
     assert not bad.any(), f"{bad.sum()} elements beyond the bound; worst ratio {(err / bound).max():.3f}"
+    if dtype == "bf16":
+        # Against runCpu's own plan of this spelling (oracle/runcpu_plan.cpp, pinned bit for bit to
+        # the op-by-op oracle): 16 rows at K = 8192. runCpu truncates every product to bf16 before
+        # its serial f32 sum, a noise of about 2^-8 |a b| per product that the matrix cores' exact
+        # products do not carry; near-zero sums differ by that noise, so the per-element bound has a
+        # floor of 0.1 max|C| (the exact product truncated once measures 0.76 of this bound on these
+        # rows), and the result must be at least as close to the float64 product as runCpu's.
+        rows = np.sort(np.random.default_rng(1).choice(8192, 16, replace=False))
+        a, b = W.gemm_inputs(8192, 8192, 8192, dtype)
+        a_rows = np.ascontiguousarray(a[rows])   # held while the C function reads it
+        ref = np.zeros((16, 8192), np.uint16)
+        plan_lib().accy_cpu_plan_mulsum(a_rows.ctypes.data, b.ctypes.data, 16, 8192, 8192, 1, ref.ctypes.data)
+        got16 = (got[rows].astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        assert_normwise(got16, ref, tol, dtype, floor=0.1)
+        assert_no_less_accurate(got16, ref, exact[rows], dtype)
 
 
 def test_c4_attention_every_head():
-    say("C4 attention f16 32 x 4096 x 4096 x 128: every head, 64 query rows each, against float64")
+    say("C4 attention f16 32 x 4096 x 4096 x 128: every query row of every head against float64")
     q, k, v = W.attention_inputs(32, 4096, 128, "f16")
     got = hip_run(W.attention_program(32, 4096, 128, "f16"), [q, k, v])[0]
-    rows = np.sort(np.random.default_rng(4).choice(4096, 64, replace=False))
     scale = float(np.float16(1.0 / math.sqrt(128)))   # the traced constant is f16
     for h in range(32):
-        qh = q[h, rows].astype(np.float64)
-        s = qh @ k[h].astype(np.float64).T * scale
-        e = np.exp(s - s.max(-1, keepdims=True))
-        exact = (e / e.sum(-1, keepdims=True)) @ v[h].astype(np.float64)
-        err = np.abs(got[h, rows].astype(np.float64) - exact).max()
-        assert err <= 2e-3 * np.abs(exact).max(), f"head {h}: normwise {err / np.abs(exact).max():.3e}"
+        kh, vh = k[h].astype(np.float64), v[h].astype(np.float64)
+        worst = 0.0
+        for r0 in range(0, 4096, 1024):
+            s = q[h, r0:r0 + 1024].astype(np.float64) @ kh.T * scale
+            e = np.exp(s - s.max(-1, keepdims=True))
+            exact = (e / e.sum(-1, keepdims=True)) @ vh
+            err = np.abs(got[h, r0:r0 + 1024].astype(np.float64) - exact)
+            # per row: within 2e-3 of the row's largest magnitude (measured about 5e-4 normwise)
+            row = err.max(-1) / np.abs(exact).max(-1)
+            assert (row <= 2e-3).all(), f"head {h}, rows {r0 + np.flatnonzero(row > 2e-3)[:4]}: {row.max():.3e}"
+            worst = max(worst, float(row.max()))
+        say(f"head {h}: worst row {worst:.2e}")
 
 
 def _bf16_const(v):

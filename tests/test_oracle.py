@@ -424,3 +424,216 @@ def test_oracle_threads_give_identical_results():
     one = oracle_run(prog, [x], threads=1)[0]
     many = oracle_run(prog, [x], threads=8)[0]
     assert np.array_equal(one, many)
+
+
+# ---- integer, compare, f64, broadcast and reshape families ----
+# Each check recomputes the expected value with Python integers or Python floats (float64), one
+# element at a time, independently of the oracle's code: a signed compare on u64, a swapped lt / gt,
+# a saturating or widened integer op, f64 evaluated through f32 or a dropped broadcast all fail.
+
+_NP_INT = {"i32": np.int32, "i64": np.int64, "u32": np.uint32, "u64": np.uint64}
+_BITS = {"i32": 32, "i64": 64, "u32": 32, "u64": 64}
+
+
+def _wrap(v, dtype):
+    """v reduced to the dtype's width (two's complement for signed types): Zig's +% -% *%."""
+    bits = _BITS[dtype]
+    v &= (1 << bits) - 1
+    if dtype[0] == "i" and v >= 1 << (bits - 1):
+        v -= 1 << bits
+    return v
+
+
+def _int_values(dtype, n, seed):
+    """Edge values of the type (both ends, around zero and, unsigned, around 2^(bits-1)) followed by
+    random values over the whole range."""
+    info = np.iinfo(_NP_INT[dtype])
+    lo, hi = int(info.min), int(info.max)
+    edges = [lo, lo + 1, hi - 1, hi, 0, 1, 2, 3]
+    if dtype[0] == "i":
+        edges += [-1, -2, -3]
+    else:
+        edges += [1 << (_BITS[dtype] - 1), (1 << (_BITS[dtype] - 1)) - 1, (1 << (_BITS[dtype] - 1)) + 1]
+    rng = np.random.default_rng(seed)
+    rand = rng.integers(lo, hi, size=n - len(edges), dtype=_NP_INT[dtype], endpoint=True)
+    return np.concatenate([np.array(edges, dtype=_NP_INT[dtype]), rand])
+
+
+@pytest.mark.parametrize("dtype", ["i32", "i64", "u32", "u64"])
+def test_integer_add_sub_mul_wrap_at_the_declared_width(dtype):
+    """evalIntBinary (src/eval/evaluator.zig:2254-2263): add, sub and mul wrap (+% -% *%)."""
+    x = _int_values(dtype, 96, 40)
+    y = np.roll(_int_values(dtype, 96, 41), 5)
+    prog = T.define("w", [T.spec(dtype, i=96)] * 2,
+                    lambda b, a: [a[0].add(a[1]), a[0].sub(a[1]), a[0].mul(a[1])])
+    add, sub, mul = oracle_run(prog, [x, y])
+    for i in range(96):
+        xi, yi = int(x[i]), int(y[i])
+        assert int(add[i]) == _wrap(xi + yi, dtype), (i, xi, yi)
+        assert int(sub[i]) == _wrap(xi - yi, dtype), (i, xi, yi)
+        assert int(mul[i]) == _wrap(xi * yi, dtype), (i, xi, yi)
+
+
+@pytest.mark.parametrize("dtype", ["i32", "i64", "u32", "u64"])
+def test_integer_max_min_elementwise_and_as_folds(dtype):
+    """@max / @min (evaluator.zig:2261-2262) on the type's own order: u64 values above 2^63 are the
+    largest, not negative. As folds (reduction.zig:1140-1155) they start from the type's lowest /
+    highest value (builder.zig:760-797; explicit inits for unsigned types) and take every element;
+    the sum fold wraps."""
+    x = _int_values(dtype, 8 * 24, 42).reshape(8, 24)
+    y = _int_values(dtype, 8 * 24, 43).reshape(8, 24)[::-1].copy()
+    info = np.iinfo(_NP_INT[dtype])
+
+    def body(b, a):
+        if dtype[0] == "i":
+            return [a[0].max(a[1]), a[0].min(a[1]), a[0].max("c"), a[0].min("c"), a[0].sum("c"), a[0].max("r")]
+        # The named max / min have no unsigned init (builder.zig:769-796): explicit inits instead.
+        lo, hi = b.full(dtype, int(info.min)), b.full(dtype, int(info.max))
+        return [a[0].max(a[1]), a[0].min(a[1]), a[0].reduce(lo, "max", "c"), a[0].reduce(hi, "min", "c"),
+                a[0].sum("c"), a[0].reduce(lo, "max", "r")]
+    prog = T.define("m", [T.spec(dtype, r=8, c=24)] * 2, body)
+    mx, mn, fmax, fmin, fsum, fmax_r = oracle_run(prog, [x, y])
+    X, Y = [[int(v) for v in row] for row in x], [[int(v) for v in row] for row in y]
+    for r in range(8):
+        for c in range(24):
+            assert int(mx[r, c]) == max(X[r][c], Y[r][c]) and int(mn[r, c]) == min(X[r][c], Y[r][c])
+        assert int(fmax[r]) == max(X[r]) and int(fmin[r]) == min(X[r])
+        assert int(fsum[r]) == _wrap(sum(X[r]), dtype)
+    for c in range(24):
+        assert int(fmax_r[c]) == max(X[r][c] for r in range(8))
+
+
+@pytest.mark.parametrize("dtype", ["i32", "u64"])
+def test_integer_dot_general_wraps_per_output(dtype):
+    """dot_general on integers (dot.zig:2049-2115 with the evaluator's wrapping add and multiply):
+    out[m, n] = sum over k of a[m, k] * b[k, n], reduced to the type's width."""
+    a = _int_values(dtype, 5 * 19, 44).reshape(5, 19)
+    bm = _int_values(dtype, 19 * 7, 45).reshape(19, 7)
+    got = oracle_run(W.gemm_program(5, 19, 7, dtype=dtype), [a, bm])[0]
+    for m in range(5):
+        for n in range(7):
+            want = _wrap(sum(int(a[m, k]) * int(bm[k, n]) for k in range(19)), dtype)
+            assert int(got[m, n]) == want, (m, n)
+    # A batched contraction with the contracted axis first in one operand.
+    p = _int_values(dtype, 3 * 4 * 6, 46).reshape(3, 4, 6)      # batch, k, m
+    q = _int_values(dtype, 3 * 5 * 4, 47).reshape(3, 5, 4)      # batch, n, k
+    prog = T.define("bd", [T.spec(dtype, batch=3, k=4, m=6), T.spec(dtype, batch=3, n=5, k=4)],
+                    lambda b, v: v[0].contract(v[1], "k"))
+    got = oracle_run(prog, [p, q])[0]
+    assert got.shape == (3, 6, 5)
+    for bi in range(3):
+        for m in range(6):
+            for n in range(5):
+                want = _wrap(sum(int(p[bi, k, m]) * int(q[bi, n, k]) for k in range(4)), dtype)
+                assert int(got[bi, m, n]) == want
+
+
+_CMP = {"lt": lambda x, y: x < y, "le": lambda x, y: x <= y, "gt": lambda x, y: x > y,
+        "ge": lambda x, y: x >= y, "eq": lambda x, y: x == y, "ne": lambda x, y: x != y}
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f64", "i32", "i64", "u32", "u64"])
+def test_all_six_compares(dtype):
+    """evalFloatCmp / evalIntCmp / evalUnsignedCmp (evaluator.zig:2454-2490): floats compare as
+    IEEE values (NaN: only ne is true; -0 == +0), signed integers by value, unsigned integers on
+    their unsigned order (u64 above 2^63 is large)."""
+    if dtype in ("f32", "f64"):
+        npd = np.float32 if dtype == "f32" else np.float64
+        base = [np.nan, -np.inf, -3.5, -1.0, -0.0, 0.0, 1e-30, 1.0, 2.5, np.inf]
+        x = np.array([u for u in base for _ in base], npd)
+        y = np.array([v for _ in base for v in base], npd)
+        X, Y = [float(v) for v in x], [float(v) for v in y]
+    else:
+        vals = _int_values(dtype, 16, 48)
+        x = np.repeat(vals, 16)
+        y = np.tile(vals, 16)
+        X, Y = [int(v) for v in x], [int(v) for v in y]
+    n = len(x)
+    names = list(_CMP)
+    prog = T.define("c", [T.spec(dtype, i=n)] * 2, lambda b, a: [a[0].compare(d, a[1]) for d in names])
+    outs = oracle_run(prog, [x, y])
+    for d, got in zip(names, outs):
+        for i in range(n):
+            assert bool(got[i]) == _CMP[d](X[i], Y[i]), (d, X[i], Y[i])
+
+
+def test_f64_arithmetic_is_float64():
+    """f64 runs evalFloatBinary / unary with f64 operands (evaluator.zig:2248-2250): add, sub, mul
+    and div are the correctly rounded float64 results bit for bit (Python floats), exp is within
+    one float64 ulp of the exact value, and an f64 sum is a serial float64 fold. Inputs are chosen
+    so that evaluating through f32 changes every result."""
+    rng = np.random.default_rng(49)
+    x = (rng.standard_normal(256) * np.exp(rng.uniform(-30, 30, 256))).astype(np.float64)
+    y = (rng.standard_normal(256) * np.exp(rng.uniform(-30, 30, 256))).astype(np.float64)
+    e = rng.uniform(-700, 700, 256)
+    prog = T.define("f", [T.spec("f64", i=256)] * 3,
+                    lambda b, a: [a[0].add(a[1]), a[0].sub(a[1]), a[0].mul(a[1]), a[0].div(a[1]), a[2].exp()])
+    add, sub, mul, div, ex = oracle_run(prog, [x, y, e])
+    for i in range(256):
+        xi, yi = float(x[i]), float(y[i])
+        assert add[i] == xi + yi and sub[i] == xi - yi and mul[i] == xi * yi and div[i] == xi / yi
+        assert float(np.float32(np.float32(xi) * np.float32(yi))) != xi * yi
+        ref = math.exp(float(e[i]))
+        assert abs(float(ex[i]) - ref) <= math.ulp(ref), (e[i], ex[i], ref)
+    s = np.array([1e16, 1.0, -1e16, 1.0, 3.0, 2.0 ** -40], np.float64)
+    got = oracle_run(T.define("s", [T.spec("f64", i=6)], lambda b, a: a[0].sum("i")), [s])[0]
+    acc = 0.0
+    for v in s:
+        acc = acc + float(v)
+    assert float(got) == acc and acc != float(np.float32(acc))
+
+
+def test_f64_dot_is_a_serial_float64_fold():
+    rng = np.random.default_rng(50)
+    a = rng.standard_normal((4, 29)) * 1e10
+    bm = rng.standard_normal((29, 3))
+    got = oracle_run(W.gemm_program(4, 29, 3, dtype="f64"), [a, bm])[0]
+    for m in range(4):
+        for n in range(3):
+            acc = 0.0
+            for k in range(29):
+                acc = acc + float(a[m, k]) * float(bm[k, n])
+            assert got[m, n] == acc
+
+
+@pytest.mark.parametrize("dtype", ["f32", "i32", "u64", "bf16"])
+def test_broadcast_op_splats_one_element_and_copies_equal_sizes(dtype):
+    """`broadcast` (builder.zig:487) lowers only from a splat (elementwise.zig:943-957): a
+    one-element operand fills the result; an operand with as many elements is copied in order."""
+    npd = T.NUMPY_DTYPE[dtype]
+    one = np.array([7], npd).reshape(())
+    six = np.arange(1, 7).astype(npd)
+    prog = T.define("bc", [T.spec(dtype), T.spec(dtype, i=6)],
+                    lambda b, a: [b.broadcast(a[0], [("r", 3), ("c", 5)]),
+                                  b.broadcast(a[1], [("r", 2), ("c", 3)])])
+    splat, copy = oracle_run(prog, [one, six])
+    assert splat.shape == (3, 5) and (splat == npd(7)).all()
+    assert copy.shape == (2, 3) and np.array_equal(copy.reshape(-1), six)
+    with pytest.raises(RuntimeError):
+        oracle_run(T.define("bad", [T.spec(dtype, i=2)], lambda b, a: b.broadcast(a[0], [("r", 4)])),
+                   [six[:2]])
+
+
+def test_split_and_merge_reshape_in_row_major_order():
+    """Value.split / merge (builder.zig:438-470; value.zig:88-99): a split is a row-major reshape of
+    one axis; a merge moves the merged axes together at the first one's position (algebra.zig:241-309)
+    and reshapes. Checked element by element against numpy's reshape / transpose, and through a
+    reduction over a split part and a contraction over a merged axis."""
+    x = np.arange(2 * 12 * 5, dtype=np.int32).reshape(2, 12, 5)
+    prog = T.define("sm", [T.spec("i32", a=2, b=12, c=5)],
+                    lambda bb, v: [v[0].split("b", p=3, q=4), v[0].merge(("c", "a"), "m"),
+                                   v[0].split("b", p=3, q=4).sum("q"), v[0].merge(("a", "b"), "m")])
+    sp, mg, red, mg2 = oracle_run(prog, [x])
+    assert np.array_equal(sp, x.reshape(2, 3, 4, 5))
+    assert np.array_equal(mg, x.transpose(2, 0, 1).reshape(10, 12))
+    for a in range(2):
+        for p in range(3):
+            for c in range(5):
+                assert int(red[a, p, c]) == sum(int(x[a, 4 * p + q, c]) for q in range(4))
+    assert np.array_equal(mg2, x.reshape(24, 5))
+    y = np.arange(10 * 3, dtype=np.int32).reshape(10, 3) - 7
+    prog = T.define("mc", [T.spec("i32", a=2, b=12, c=5), T.spec("i32", m=10, n=3)],
+                    lambda bb, v: v[0].merge(("c", "a"), "m").contract(v[1], "m"))
+    got = oracle_run(prog, [x, y])[0]
+    want = x.transpose(2, 0, 1).reshape(10, 12).astype(np.int64).T @ y.astype(np.int64)
+    assert np.array_equal(got, want.astype(np.int32))

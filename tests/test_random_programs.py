@@ -1,6 +1,6 @@
 """Differential test over seeded random programs: elementwise chains, named-axis broadcasts and
-transposes (aligned binaries), compare / select, and reductions over one or two axes, in f32 and
-i32, on extents that are and are not multiples of four. Each program runs on the target and on the
+transposes (aligned binaries), compare / select, reductions over one or two axes, extent-changing
+reshapes (split / merge) and the `broadcast` op (a splat or an equal-size copy), in f32 and i32, on extents that are and are not multiples of four. Each program runs on the target and on the
 oracle (the runCpu restatement): integer results bit-exact; f32 results within 1e-5 of the largest
 magnitude of the output (reductions may be associated differently, and the values stay in a moderate
 range: no exp / log, divisions by |x| + 1). The same for random contraction programs (matrix-core
@@ -27,8 +27,38 @@ def _program(seed, dtype):
         for _ in range(int(rng.integers(3, 8))):
             x = vals[int(rng.integers(len(vals)))]
             y = vals[int(rng.integers(len(vals)))]
-            op = str(rng.choice(["add", "sub", "mul", "max", "min", "neg", "abs", "div", "select", "sum", "rmax"]))
-            if op in ("add", "sub", "mul", "max", "min"):
+            op = str(rng.choice(["add", "sub", "mul", "max", "min", "neg", "abs", "div", "select", "sum", "rmax",
+                                 "split", "merge", "splat"]))
+            names = [n for n, _ in x.ty.dims]
+            if op == "split":
+                # An extent-changing reshape pair (builder.zig:438-470): axis n split as (hi, lo), then
+                # merged back in the order (lo, hi), which permutes n's elements.
+                cand = [(n, e, p) for n, e in x.ty.dims for p in (2, 3, 4, 5, 13) if e % p == 0 and e > p]
+                if cand:
+                    n, e, p = cand[int(rng.integers(len(cand)))]
+                    v = x.split(n, (n + "h", p), (n + "l", e // p)).merge((n + "l", n + "h"), n)
+                else:
+                    v = x.neg()
+            elif op == "merge":
+                # Two axes merged in a random order, then either split back (a transpose of x through
+                # reshapes) or reduced over the merged axis.
+                if len(names) >= 2:
+                    u, w = (str(t) for t in rng.choice(names, size=2, replace=False))
+                    m = x.merge((u, w), "m")
+                    if rng.random() < 0.5 or len(names) == 2:
+                        v = m.split("m", (u, x.ty.dims[names.index(u)][1]), (w, x.ty.dims[names.index(w)][1]))
+                    else:
+                        v = m.sum("m") if rng.random() < 0.5 else m.max("m")
+                else:
+                    v = x.abs()
+            elif op == "splat":
+                # The `broadcast` op (builder.zig:487): a one-element value spread over y's axes, or an
+                # equal-size value copied in order into reversed axes.
+                if rng.random() < 0.5:
+                    v = b.broadcast(x.max(tuple(names)), y.ty.dims).add(y)
+                else:
+                    v = b.broadcast(x, tuple(reversed(x.ty.dims)))
+            elif op in ("add", "sub", "mul", "max", "min"):
                 v = getattr(x, op)(y)
             elif op == "neg":
                 v = x.neg()
@@ -38,8 +68,9 @@ def _program(seed, dtype):
                 v = x.div(y.abs().add(one)) if dtype == "f32" else x.div(y.abs().add(one))
             elif op == "select":
                 v = x.compare("gt", y).select(x, y.neg())
+            elif not names:
+                v = x.neg()                       # nothing left to reduce over
             else:
-                names = [n for n, _ in x.ty.dims]
                 k = int(rng.integers(1, len(names) + 1)) if len(names) > 1 else 1
                 axes = tuple(rng.choice(names, size=min(k, len(names)), replace=False))
                 if len(axes) == len(names):
@@ -213,3 +244,16 @@ def test_random_scan_programs_match_the_oracle(seed, dtype):
             # f32 sums are associated differently on the target; the carries feed them back each step
             scale = float(np.abs(r).max()) if r.size else 0.0
             assert np.all(np.abs(g.astype(np.float64) - r) <= 1e-4 * max(scale, 1e-30)), f"output {i}"
+
+
+def test_random_programs_draw_reshapes_and_broadcasts():
+    """At least a third of the seeds of the elementwise family carry an extent-changing reshape
+    (split / merge) or a `broadcast` op, so the GPU differential test covers them."""
+    drawn = 0
+    for dtype in ("f32", "i32"):
+        for seed in SEEDS:
+            prog, _ = _program(seed, dtype)
+            ops = prog.operations
+            drawn += any(op.kind == "broadcast" or (op.kind == "reshape" and prog.type_of(op.args[0]).shape
+                                                    != op.result.shape) for op in ops)
+    assert drawn >= 2 * len(SEEDS) / 3, drawn

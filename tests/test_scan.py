@@ -181,7 +181,8 @@ def test_scan_program_invoked_repeatedly_reuses_its_carry_buffers():
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", ["relax", "power", "count"])
 def test_long_scans_invoked_repeatedly(case):
-    """Loops of 70-100 iterations against the oracle, the same executor invoked three times with
+    """Loops of 40-100 iterations (relaxation 100, matrix power 40, counter 70) against the oracle,
+    the same executor invoked three times with
     another program's work and a synchronisation between the invocations; every invocation equals
     the first bit for bit."""
     if case == "relax":

@@ -110,3 +110,109 @@ def test_scratch_entry_point_refuses_programs_beyond_the_scratch():
         dummy.free()
     finally:
         s.release(h)
+
+
+# ---- HIP graph capture ----
+
+def _hip_runtime():
+    """The HIP runtime the library links (stream capture and graph calls are not part of its C ABI)."""
+    rt = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so")
+    vp = ctypes.c_void_p
+    rt.hipStreamBeginCapture.argtypes = [vp, ctypes.c_int]
+    rt.hipStreamEndCapture.argtypes = [vp, ctypes.POINTER(vp)]
+    rt.hipGraphInstantiate.argtypes = [ctypes.POINTER(vp), vp, vp, ctypes.c_char_p, ctypes.c_size_t]
+    rt.hipGraphLaunch.argtypes = [vp, vp]
+    rt.hipGraphExecDestroy.argtypes = [vp]
+    rt.hipGraphDestroy.argtypes = [vp]
+    for f in ("hipStreamBeginCapture", "hipStreamEndCapture", "hipGraphInstantiate", "hipGraphLaunch",
+              "hipGraphExecDestroy", "hipGraphDestroy"):
+        getattr(rt, f).restype = ctypes.c_int
+    return rt
+
+
+class _Bound:
+    """Device copies of one invocation's inputs and outputs, kept for several invocations."""
+
+    def __init__(self, prog, ins):
+        self.dins = [hip.DeviceBuffer.from_array(x) for x in ins]
+        self.outs = [np.zeros(t.shape, T.NUMPY_DTYPE[t.dtype]) for t in prog.output_types()]
+        self.douts = [hip.DeviceBuffer(max(o.nbytes, 1)) for o in self.outs]
+        self.ip = (ctypes.c_void_p * max(len(self.dins), 1))(*[d.ptr for d in self.dins])
+        self.op = (ctypes.c_void_p * max(len(self.douts), 1))(*[d.ptr for d in self.douts])
+
+    def call(self, h, scratch, stream):
+        lib = hip.library()
+        fn = lib.accy_hip_invoke_device_scratch if scratch else lib.accy_hip_invoke_device
+        st = fn(h, self.ip, len(self.dins), self.op, len(self.douts), ctypes.c_void_p(stream.handle))
+        assert st == hip.OK, lib.accy_hip_last_error().decode()
+
+    def clear(self):
+        for o, d in zip(self.outs, self.douts):
+            d.upload(np.zeros_like(o))
+
+    def read(self):
+        return [d.download(np.zeros_like(o)) for o, d in zip(self.outs, self.douts)]
+
+    def free(self):
+        for d in self.dins + self.douts:
+            d.free()
+
+
+def _capture(rt, stream, fn):
+    graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+    assert rt.hipStreamBeginCapture(ctypes.c_void_p(stream.handle), 1) == 0   # thread-local mode
+    fn()
+    assert rt.hipStreamEndCapture(ctypes.c_void_p(stream.handle), ctypes.byref(graph)) == 0
+    return graph
+
+
+def _same(got, ref):
+    for g, r in zip(got, ref):
+        assert g.shape == r.shape and np.array_equal(g.view(np.uint8), r.view(np.uint8))
+
+
+@pytest.mark.parametrize("scratch", [False, True])
+def test_invocations_captured_into_hip_graphs(scratch):
+    """A decoder block whose MLP-up epilogue is a lookup table filled by a run-once kernel. The first
+    invocation of a fresh executor is captured into a graph that is destroyed without being launched;
+    a later eager invocation must still find the table filled. Then an invocation (invoke_device, or
+    the allocation-free variant) is captured and the graph replayed three times, with eager work of
+    another program between the replays (which, on the scratch path, overwrites the shared scratch);
+    every replay must equal an eager invoke_device of a separately compiled executor bit for bit."""
+    prog = W.decoder_program(1, 256, 256, 2, 128, 512)
+    assert "accy_lut_" in hip.plan_source(prog)
+    other = W.decoder_program(1, 128, 256, 2, 128, 512)
+    rt = _hip_runtime()
+    s, stream = hip.Session(), hip.Stream()
+    ins = _inputs(prog, seed=30)
+    href = s.compile(prog)
+    ref = _run(s, href, prog, ins, False, stream)
+    s.release(href)
+    h, ho = s.compile(prog), s.compile(other)
+    bound, obound = _Bound(prog, ins), _Bound(other, _inputs(other, seed=31))
+    try:
+        print(f"capture of the first invocation, scratch={scratch}", flush=True)
+        rt.hipGraphDestroy(_capture(rt, stream, lambda: bound.call(h, scratch, stream)))
+        bound.clear()
+        bound.call(h, False, stream)
+        stream.synchronize()
+        _same(bound.read(), ref)
+        graph = _capture(rt, stream, lambda: bound.call(h, scratch, stream))
+        exe = ctypes.c_void_p()
+        assert rt.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for r in range(3):
+            print(f"replay {r}", flush=True)
+            bound.clear()
+            assert rt.hipGraphLaunch(exe, ctypes.c_void_p(stream.handle)) == 0
+            stream.synchronize()
+            _same(bound.read(), ref)
+            obound.call(ho, scratch, stream)
+            stream.synchronize()
+        rt.hipGraphExecDestroy(exe)
+        rt.hipGraphDestroy(graph)
+    finally:
+        bound.free()
+        obound.free()
+        s.release(h)
+        s.release(ho)
+        stream.destroy()

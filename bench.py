@@ -46,7 +46,9 @@ from accy_amd import workloads as W  # noqa: E402
 
 METRIC = "GB/s & TFLOP/s per config as % of MI355X roofline; speedup vs runCpu"
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2500.0, "f16": 2500.0}
+# Dense peaks of MI355X as BASELINE.md's roofline table states them (bf16 / f16 2516.6 TFLOP/s: 256 CUs x
+# 4 SIMDs x 1024 FLOP per clock x 2.4 GHz).
+MFMA_PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6, "f16": 2516.6}
 VALU_PEAK_TFLOPS = 157.3
 
 
@@ -136,6 +138,17 @@ def config_table():
                                      lambda b, a: a[0].mul(b.full_float(T.Type("f32", ()), 1.0))),
                             W.logsumexp_inputs(1024, 8192, seed=2), 2 * 1024 * 8192 * 4),
             sample_desc="1024 rows", workload=dict(rows=32768, features=8192)),
+        # Not a measured config: a kernel with almost no work (y = x * 1 over 64 f32, one workgroup),
+        # whose GRBM_GUI_ACTIVE reading is the counter window around a dispatch beyond the kernel itself.
+        "calib-empty": dict(
+            make=lambda: (T.define("empty", [T.spec("f32", i=64)],
+                                   lambda b, a: a[0].mul(b.full_float(T.Type("f32", ()), 1.0))),
+                          [np.arange(64, dtype=np.float32)]),
+            dtype="f32", unit="GB/s", bound="hbm", work=2 * 64 * 4, peak=HBM_PEAK_GBS,
+            sample=lambda: (T.define("empty", [T.spec("f32", i=64)],
+                                     lambda b, a: a[0].mul(b.full_float(T.Type("f32", ()), 1.0))),
+                            [np.arange(64, dtype=np.float32)], 2 * 64 * 4),
+            sample_desc="64 elements", workload=dict(elements=64)),
         "c5-decoder": dict(
             make=lambda: (W.decoder_program(), W.decoder_inputs()),
             dtype="bf16", unit="TFLOP/s", bound="mfma", work=decoder_flops(4, 2048, 2048, 16, 128, 8192), peak=MFMA_PEAK_TFLOPS["bf16"],
@@ -144,10 +157,23 @@ def config_table():
     }
 
 
+CPU_SHARE = 16   # host threads one GPU's job may use on the measurement boxes
+
+
+def host_cores() -> dict:
+    """What the host reports: `nproc` (the cores this process may run on) and os.cpu_count()."""
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count() or 1
+    return dict(nproc=nproc, cpu_count=os.cpu_count() or 1)
+
+
 def cpu_threads() -> int:
-    """Host threads for the CPU legs: $ACCY_CPU_THREADS, else the host's cores capped at 16 (the CPU
-    share of one GPU on the measurement boxes)."""
-    return min(int(os.environ.get("ACCY_CPU_THREADS", "0")) or (os.cpu_count() or 1), 16)
+    """Host threads for the CPU legs: $ACCY_CPU_THREADS, else `nproc` capped at 16. The boxes this
+    runs on give one GPU's job a share of 16 host threads whatever `nproc` reports (the rest belong to
+    the other GPUs' jobs), so more threads would time contention, not runCpu."""
+    return min(int(os.environ.get("ACCY_CPU_THREADS", "0")) or host_cores()["nproc"], CPU_SHARE)
 
 
 def plan_runner(name: str, lib, prog, ins):
@@ -216,7 +242,10 @@ def oracle_time(name: str, cfg, budget_s: float):
     t_all, n_all = timed(threads)
     t_one, n_one = timed(1)
     lib.accy_cpu_set_threads(threads)
+    hc = host_cores()
     return dict(value=work / t_all / scale, unit=cfg["unit"], cores=threads, kind="port", plan=plan,
+                nproc=hc["nproc"], cpu_count=hc["cpu_count"],
+                cores_note=f"min(nproc, {CPU_SHARE}): the host-thread share of one GPU's job on these boxes",
                 sample=f"{cfg['sample_desc']}; median of {n_all} runs, {t_all:.3f} s each",
                 single_core=dict(value=work / t_one / scale, cores=1,
                                  sample=f"median of {n_one} runs, {t_one:.3f} s each"))
@@ -298,7 +327,7 @@ def measure(name: str, cfg: dict, steps: int, warmup: int, warmup_s: float) -> d
     for b in dins + douts:
         b.free()
     stream.destroy()
-    return dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"], warmup=done,
+    return dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"], warmup_run=done,
                 workload=dict(workload=name, **cfg["workload"]), roofline=roof,
                 kernels={lbl: float(k.mean_ms) for lbl, k in per_kernel.items()})
 
@@ -315,7 +344,8 @@ def main() -> int:
     # contraction goes from about 0.82 to 1.08 ms per launch within four launches, the C2 row kernel
     # from 0.156 to 0.213 ms within 20) and then settles over some milliseconds. Warmup runs at least
     # --warmup steps and at least --warmup-seconds of them, so the timed steps measure the sustained
-    # steady state; the line reports the number of warmup steps actually run.
+    # steady state. The line reports the requested --warmup as `warmup` and the steps actually run as
+    # `warmup_steps_run`.
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--warmup-seconds", type=float, default=0.2)
     ap.add_argument("--config", default="all",
@@ -341,14 +371,15 @@ def main() -> int:
     h = results[head]
     line = {
         "metric": METRIC, "value": h["value"], "unit": h["unit"], "n_gpus": 1, "steps": args.steps,
-        "warmup": h["warmup"], "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "warmup_steps_run": h["warmup_run"], "warmup_seconds": args.warmup_seconds,
+        "ms_per_step": h["ms_per_step"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": h["dtype"], "data": "synthetic (seeded SplitMix64)",
         "config": h["workload"], "roofline": h["roofline"], "cpu_baseline": h["cpu_baseline"],
         "kernels": h["kernels"],
     }
     if len(names) > 1:
         line["configs"] = {
-            n: dict(ms=r["ms_per_step"], value=r["value"], unit=r["unit"], dtype=r["dtype"], warmup=r["warmup"],
+            n: dict(ms=r["ms_per_step"], value=r["value"], unit=r["unit"], dtype=r["dtype"], warmup_steps_run=r["warmup_run"],
                     bound=r["roofline"]["bound"],
                     kernel=r["roofline"]["kernel"], kernel_ms=r["roofline"]["kernel_ms"],
                     achieved=r["roofline"]["achieved"], peak=r["roofline"]["peak"],

@@ -787,6 +787,31 @@ int accy_cpu_wire_roundtrip(const uint8_t* wire_bytes, size_t wire_len, uint8_t*
   }
 }
 
+// Decodes wire bytes with the shared codec and writes the type the decoder's checked builder derived
+// for every value, one line each ("<depth> <kind> <dtype>{name=extent,...}"), scan bodies after their
+// scan at depth + 1. Tests compare these with the types the Python tracer derived on its own while
+// recording, so a wrong derivation in the decoder (shared with the product) cannot go unseen.
+static void dump_types(const Graph& g, int depth, std::string& out) {
+  for (const Op& op : g.ops) {
+    out += std::to_string(depth) + " " + kind_name(op.kind) + " " + op.result.str() + "\n";
+    if (op.body) dump_types(*op.body, depth + 1, out);
+  }
+}
+
+int accy_cpu_wire_types(const uint8_t* wire_bytes, size_t wire_len, char* out, size_t cap, size_t* needed) {
+  try {
+    Program prog = wire::decode(wire_bytes, wire_len);
+    std::string text;
+    dump_types(prog, 0, text);
+    if (needed) *needed = text.size() + 1;
+    if (out && cap > text.size()) std::memcpy(out, text.c_str(), text.size() + 1);
+    return 0;
+  } catch (const Error& e) {
+    g_error = e.what();
+    return e.code == Err::UnsupportedVersion ? 2 : 1;
+  }
+}
+
 // Name of the error the last failing decode raised (e.g. "BadMagic").
 const char* accy_cpu_error_name(void) {
   size_t colon = g_error.find(':');

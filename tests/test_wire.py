@@ -1,4 +1,5 @@
 """Tracer and ACTP v1 wire format (src/tensor/trace/builder.zig, src/tensor/wire/*.zig)."""
+import ctypes
 import struct
 
 import numpy as np
@@ -6,7 +7,7 @@ import pytest
 
 from accy_amd import tensor as T
 from accy_amd import workloads as W
-from conftest import wire_roundtrip
+from conftest import oracle_lib, wire_roundtrip
 
 
 def u32(v):
@@ -162,3 +163,53 @@ def test_recording_errors(make, err):
     with pytest.raises(T.TensorError) as e:
         make(T.Builder("e"))
     assert e.value.name == err
+
+
+# ---- the decoder's derived types against the tracer's (the oracle shares the decoder) ----
+
+def _python_types(prog, depth=0):
+    out = []
+    for op in prog.operations:
+        dims = ",".join(f"{n}={e}" for n, e in op.result.dims)
+        out.append(f"{depth} {op.kind} {op.result.dtype}{{{dims}}}")
+        if op.body is not None:
+            out.extend(_python_types(op.body, depth + 1))
+    return out
+
+
+def _decoder_types(wire: bytes):
+    lib = oracle_lib()
+    lib.accy_cpu_wire_types.argtypes = [ctypes.POINTER(ctypes.c_uint8), ctypes.c_size_t, ctypes.c_char_p,
+                                        ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    need = ctypes.c_size_t()
+    buf = (ctypes.c_uint8 * len(wire)).from_buffer_copy(wire)
+    assert lib.accy_cpu_wire_types(buf, len(wire), None, 0, ctypes.byref(need)) == 0
+    out = ctypes.create_string_buffer(need.value)
+    assert lib.accy_cpu_wire_types(buf, len(wire), out, need.value, ctypes.byref(need)) == 0
+    return out.value.decode().splitlines()
+
+
+def _type_corpus():
+    import test_random_programs as R
+    progs = [W.tone_program(8192, 16384), W.logsumexp_program(32768, 8192),
+             W.gemm_program(8192, 8192, 8192, "bf16", "mulsum"), W.gemm_program(64, 32, 16, "f32", "contract"),
+             W.attention_program(32, 4096, 128, "f16"), W.attention_program(2, 256, 64, "bf16", causal=True),
+             W.decoder_program(), W.decoder_program(2, 8, 16, 2, 8, 32, dtype="f32")]
+    progs += [R._program(s, d)[0] for s in range(40) for d in ("f32", "i32")]
+    progs += [R._contraction_program(s, d)[0] for s in range(24) for d in ("f32", "bf16")]
+    progs += [R._scan_program(s, d)[0] for s in range(16) for d in ("f32", "i32")]
+    return progs
+
+
+def test_decoder_derives_the_same_types_as_the_tracer():
+    """The C++ decoder replays every operation through its own checked builder; the Python tracer
+    derived every type independently while recording (tensor.py). Both must give every value of every
+    program, scan bodies included, the same dtype, axis names and extents: the oracle and the target
+    share the decoder, so this is what pins its type derivation."""
+    n = 0
+    for prog in _type_corpus():
+        want = _python_types(prog)
+        got = _decoder_types(prog.encode())
+        assert got == want, prog.name
+        n += len(want)
+    assert n > 2500

@@ -7,6 +7,7 @@ against the float64 formula; integer, index and i1 results, and 16-bit add/sub/m
 bit-exact.
 """
 import math
+import re
 
 import numpy as np
 import pytest
@@ -447,8 +448,9 @@ def test_gemm_direct_to_lds_layouts(case):
 
 
 def _gemm_kernels(prog):
+    """The contraction kernel templates a program's plan instantiates (accy::gemm::<kernel><Cfg_...>)."""
     src = hip.plan_source(prog.encode(), compile=False)
-    return [l.split("accy::gemm::")[1].split("<")[0] for l in src.splitlines() if "accy::gemm::" in l]
+    return re.findall(r"accy::gemm::(\w+)<Cfg_", src)
 
 
 @pytest.mark.parametrize("m,k,n,spelling", [(512, 96, 256, "contract"), (256, 64, 512, "mulsum"),

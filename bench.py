@@ -13,9 +13,8 @@
   bytes per launch measured with rocprofv3 counters (FETCH_SIZE, WRITE_SIZE, calibrated on a copy
   kernel) and committed in profiles/traffic.json; null for a workload not measured there.
 * ``cpu_baseline`` is the runCpu restatement (oracle/) timed on this host on a bounded sample of the
-  same workload, then scaled to the metric's unit (kind "port"): for C1-C4 runCpu's kernel plan as
-  fused loops (oracle/runcpu_plan.cpp), for C5 the op-by-op oracle; all host threads (at most 16)
-  and one thread.
+  same workload, then scaled to the metric's unit (kind "port"): runCpu's kernel plan as fused loops
+  (oracle/runcpu_plan.cpp); min(nproc, 16) host threads and one thread.
 
 The headline workload is C2 (row-wise logsumexp, x f32[32768, 8192]), the configuration the metric
 is quoted on that fits one GPU: ``value``, ``roofline`` and ``cpu_baseline`` are C2's. The default run
@@ -178,9 +177,9 @@ def cpu_threads() -> int:
 
 def plan_runner(name: str, lib, prog, ins):
     """The CPU baseline's computation for one config: runCpu's kernel plan as fused loops
-    (oracle/runcpu_plan.cpp: no intermediate is materialised; each output's arithmetic is the op-by-op
-    oracle's, which tests/test_cpu_plan.py checks bit for bit) for C1-C4, the op-by-op oracle
-    otherwise. Returns (callable, description)."""
+    (oracle/runcpu_plan.cpp: intermediates only where the plan has them; each output's arithmetic is
+    the op-by-op oracle's, which tests/test_cpu_plan.py checks bit for bit) for C1-C5, the op-by-op
+    oracle otherwise. Returns (callable, description)."""
     vp, i64 = ctypes.c_void_p, ctypes.c_int64
     ptr = lambda x: ctypes.c_void_p(x.ctypes.data)
     if name == "c1-tone":
@@ -210,6 +209,15 @@ def plan_runner(name: str, lib, prog, ins):
         return (lambda: lib.accy_cpu_plan_attention_f16(ptr(q), ptr(k), ptr(v), q.shape[0], q.shape[1], q.shape[2],
                                                          scale, 0, ptr(out)),
                 "per query row: scores, per-op f16 softmax, P.V (runCpu's operations, f16 extension)")
+    if name == "c5-decoder":
+        B, S, M = ins[0].shape
+        H, D = ins[2].shape[1], ins[2].shape[2]
+        FF = ins[7].shape[1]
+        out = np.zeros((B, S, M), np.uint16)
+        lib.accy_cpu_plan_decoder_bf16.argtypes = [vp] * 9 + [i64] * 6 + [vp]
+        return (lambda: lib.accy_cpu_plan_decoder_bf16(*[ptr(a) for a in ins], B, S, M, H, D, FF, ptr(out)),
+                "norm rows with the squared prologue fused, serial-k dots, per-row causal softmax, GELU, "
+                "residuals (runCpu's plan, bf16 extension)")
     sys.path.insert(0, str(ROOT / "tests"))
     from conftest import oracle_run
     return (lambda: oracle_run(prog, ins)), "op-by-op oracle (every intermediate materialised)"

@@ -74,3 +74,21 @@ def test_plans_give_the_same_bits_on_one_and_many_threads():
     l.accy_cpu_set_threads(8)
     l.accy_cpu_plan_logsumexp(p(x), 64, 512, p(many))
     assert np.array_equal(one, many)
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 16, 2, 8, 32), (1, 24, 64, 4, 16, 96)])
+def test_decoder_plan_equals_oracle(shape):
+    """The C5 block's plan (norm rows with the squared prologue fused, serial-k dots, per-row causal
+    softmax, GELU, residuals) gives the op-by-op oracle's bits, with inputs of the benchmark's
+    distribution and a row scaled so that the norms and softmax see large values."""
+    B, S, M, H, D, FF = shape
+    ins = W.decoder_inputs(B, S, M, H, D, FF, seed=12)
+    x = W.bf16_to_f32(ins[0]).copy()
+    x[0, 1] *= 40.0
+    ins[0] = W.to_dtype(x, "bf16")
+    out = np.zeros((B, S, M), np.uint16)
+    l = lib()
+    l.accy_cpu_plan_decoder_bf16.argtypes = [F] * 9 + [I] * 6 + [F]
+    l.accy_cpu_plan_decoder_bf16(*[p(a) for a in ins], B, S, M, H, D, FF, p(out))
+    ref = oracle_run(W.decoder_program(B, S, M, H, D, FF), ins)[0]
+    assert np.array_equal(out, ref)

@@ -201,6 +201,7 @@ Executor::Executor(Program program, Plan plan) : program_(std::move(program)), p
     }
     if (any_once) check(hipStreamSynchronize(stream_), "hipStreamSynchronize");
   } catch (...) {
+    if (stream_) (void)hipStreamSynchronize(stream_);  // a run-once kernel may still be running
     for (void* p : owned_)
       if (p) (void)hipFree(p);
     for (auto& bufs : loop_bufs_)

@@ -976,3 +976,25 @@ def test_bad_wire_is_refused_by_compile():
     with pytest.raises(hip.HipError) as e:
         hip.Session().compile(b"ACTP\x02\x00\x00\x00")
     assert e.value.status == hip.UNSUPPORTED_VERSION
+
+
+@pytest.mark.parametrize("rows,cols,dtype", [(4097, 1000, "f32"), (1025, 2048, "bf16"), (2050, 300, "f32")])
+def test_row_kernels_four_rows_per_workgroup(rows, cols, dtype):
+    """Short rows, many of them, run one wave per row and four rows per workgroup: a row count that is
+    not a multiple of four (the last workgroup's extra waves have no row), row lengths that leave a
+    tail inside the wave's element loop, and several passes over the cached row (a softmax: max, sum,
+    every element; an RMS norm: sum of squares, every element)."""
+    say(f"rows {rows} x {cols} {dtype}")
+    def softmax(b, a):
+        e = a[0].sub(a[0].max("c")).exp()
+        return e.div(e.sum("c"))
+    prog = T.define("sm", [T.spec(dtype, r=rows, c=cols)], softmax)
+    assert "threadIdx.x >> 6" in hip.plan_source(prog.encode(), compile=False)
+    x = W.to_dtype(W.normal(41, rows * cols), dtype).reshape(rows, cols)
+    got, ref = hip_run(prog, [x])[0], oracle_run(prog, [x])[0]
+    assert_rel(got, ref, 1e-5 if dtype == "f32" else 2e-2, dtype)
+    norm = T.define("rms", [T.spec(dtype, r=rows, model=cols), T.spec(dtype, model=cols)],
+                    lambda b, a: W.rms_norm(b, a[0], a[1], "model", dtype))
+    g = W.to_dtype(W.uniform(42, cols, 0.5, 1.5), dtype)
+    got, ref = hip_run(norm, [x, g])[0], oracle_run(norm, [x, g])[0]
+    assert_rel(got, ref, 1e-5 if dtype == "f32" else 2e-2, dtype)

@@ -246,14 +246,19 @@ KernelStep Planner::gen_row(const RowShape& rs, const RowKernel& rk, bool commit
   uint64_t tn = prod(rs.T, 0, rs.T.size()), kn = prod(rs.K, 0, rs.K.size());
   const uint32_t VEC = tn % 4 == 0 ? 4 : 1;
   uint64_t lanes = (tn + VEC - 1) / VEC;
-  uint32_t B = lanes >= 256 ? 256 : (uint32_t)std::max<uint64_t>(64, (lanes + 63) / 64 * 64);
+  // Two waves per row: against one workgroup of four waves per row, C2's logsumexp went from 163-165 to
+  // 159-161 µs and C1's tone from 58 to 56 µs on one box (four rounds), 162.0 -> 159.0 and 53.4 ->
+  // 52.3 µs on another, and C2 161.5 -> 162.9 (C1 51.0 -> 50.2) on a third; 512 threads helped C2
+  // alike but slowed C1 by 4 %, 1024 slowed C2 by 40 %. More workgroups per CU are in flight, each
+  // meeting two waves at its barriers instead of four.
+  uint32_t B = lanes >= 128 ? 128 : (uint32_t)std::max<uint64_t>(64, (lanes + 63) / 64 * 64);
   uint64_t E = (tn + (uint64_t)B * VEC - 1) / ((uint64_t)B * VEC);
   size_t passes = rk.reduces.size() + (rk.full_vals.empty() ? 0 : 1);
   // A row read by several passes is kept in registers when each thread holds at most 64 of its
-  // elements; a row too long for that with 256 threads takes 512 or 1024 threads if that makes it
+  // elements; a row too long for that with 128 threads takes 256, 512 or 1024 threads if that makes it
   // fit (read once instead of once per pass; four waves per SIMD still have 128 registers each).
   if (passes >= 2 && E * VEC > 64) {
-    for (uint32_t wide : {512u, 1024u}) {
+    for (uint32_t wide : {256u, 512u, 1024u}) {
       const uint64_t e = (tn + (uint64_t)wide * VEC - 1) / ((uint64_t)wide * VEC);
       if (e * VEC <= 64) {
         B = wide;

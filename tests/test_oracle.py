@@ -637,3 +637,30 @@ def test_split_and_merge_reshape_in_row_major_order():
     got = oracle_run(prog, [x, y])[0]
     want = x.transpose(2, 0, 1).reshape(10, 12).astype(np.int64).T @ y.astype(np.int64)
     assert np.array_equal(got, want.astype(np.int32))
+
+
+def test_iota_broadcast_in_dim_transpose_and_select_against_numpy():
+    """iota along one axis of a 2-D shape; an aligned binary of [a, b] with [b] (broadcast_in_dim) and
+    with [b, a] (transpose, then elementwise, builder.zig:476-485); select on a compare; integer neg and
+    abs wrapping at the most negative value."""
+    prog = T.define("ib", [T.spec("f32", a=3, b=5), T.spec("f32", b=5), T.spec("f32", b=5, a=3),
+                           T.spec("i32", i=6)],
+                    lambda bb, v: [bb.iota("i32", "b", ("a", 3), ("b", 5)), bb.iota("f32", "a", ("a", 3), ("b", 5)),
+                                   v[0].add(v[1]), v[0].sub(v[2]),
+                                   v[0].compare("lt", v[2]).select(v[0], v[2].neg()),
+                                   v[3].neg(), v[3].abs()])
+    rng = np.random.default_rng(51)
+    x = rng.standard_normal((3, 5)).astype(np.float32)
+    y = rng.standard_normal(5).astype(np.float32)
+    z = rng.standard_normal((5, 3)).astype(np.float32)
+    w = np.array([0, 1, -1, 7, 2 ** 31 - 1, -(2 ** 31)], np.int32)
+    ib, ia, add, sub, sel, neg, ab = oracle_run(prog, [x, y, z, w])
+    assert np.array_equal(ib, np.broadcast_to(np.arange(5, dtype=np.int32), (3, 5)))
+    assert np.array_equal(ia, np.broadcast_to(np.arange(3, dtype=np.float32)[:, None], (3, 5)))
+    for i in range(3):
+        for j in range(5):
+            assert add[i, j] == np.float32(x[i, j] + y[j])
+            assert sub[i, j] == np.float32(x[i, j] - z[j, i])
+            assert sel[i, j] == (x[i, j] if x[i, j] < z[j, i] else -z[j, i])
+    assert [int(v) for v in neg] == [_wrap(-int(v), "i32") for v in w]
+    assert [int(v) for v in ab] == [_wrap(abs(int(v)), "i32") for v in w]

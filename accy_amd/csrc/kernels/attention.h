@@ -84,23 +84,21 @@ struct TileOffsets {
   static constexpr int DS = HD / 16, DTN = HD / 32, PER = HD / 16 / WAVES;
   static constexpr int LPR = HD / 8, RPI = 64 / LPR;  // lanes per 16-byte-chunked row, rows per load
   u32_t kf[DS];   // K fragment (A operand of S^T) of head-dim step dd: row lane % 32, chunk 2 dd + lane / 32
-                  // (LDS address in stage 0)
   u32_t vf[DTN];  // V^T fragment (ds_read_b64_tr_b16) of head-dim tile dt, for key step 0, half 0
-                  // (LDS address in stage 0)
   u32_t kg[PER];  // this lane's 16-byte chunk of K load i in global memory, and its LDS position
   u32_t vg[PER];
 
-  __device__ __forceinline__ void init(int wave, int lane, u32_t kbase, u32_t vbase) {
+  __device__ __forceinline__ void init(int wave, int lane) {
     const int row = lane & 31;
 #pragma unroll
-    for (int dd = 0; dd < DS; ++dd) kf[dd] = kbase + 2u * (u32_t)(row * HD + (((2 * dd + (lane >> 5)) ^ k_swizzle<HD>(row)) << 3));
+    for (int dd = 0; dd < DS; ++dd) kf[dd] = 2u * (u32_t)(row * HD + (((2 * dd + (lane >> 5)) ^ k_swizzle<HD>(row)) << 3));
     // V^T fragment: lanes 16 g + i read key 4 (g / 2) + i / 4 (+ 16 s + 8 r for key step s, half r, which
     // the swizzle does not see) at column unit 2 dt + (g & 1), element 4 (i & 3)
     const int g = lane >> 4, i = lane & 15, k = 4 * (g >> 1) + (i >> 2);
 #pragma unroll
     for (int dt = 0; dt < DTN; ++dt) {
       const int unit = (2 * dt + (g & 1)) ^ v_swizzle<HD>(k);
-      vf[dt] = vbase + 2u * (u32_t)(k * HD + unit * 16 + 4 * (i & 3));
+      vf[dt] = 2u * (u32_t)(k * HD + unit * 16 + 4 * (i & 3));
     }
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
@@ -126,68 +124,22 @@ __device__ __forceinline__ void dma_share(const u16_t* __restrict__ g, long firs
   for (int j = 0; j < PER; ++j) gemm::dma16(base + go[j], (ACCY_LDS void*)(lds + (wave * PER + j) * 512));
 }
 
-// Fragment reads are inline assembly, and each MFMA that consumes one first waits with an exact
-// s_waitcnt lgkmcnt(n) (n = the LDS reads issued after it, known at compile time, see lgkm_wait).
-// (With the compiler's own reads, a ds_read_b64_tr_b16 issued after a ds_read_b128 made its wait for
-// the earlier read an lgkmcnt(0), so every wait also covered the reads just issued and the fragment
-// prefetch collapsed to about one MFMA.) The stages of each operand are one LDS array, so a stage
-// and a key step are immediate offsets of the read; the lane's address (array base + position in the
-// tile) is a register computed once per query block. No other LDS access and no scalar memory load
-// (whose returns are unordered) is in flight while a step's reads are pending.
-constexpr int kStageBytes(int hd) { return BK * hd * 2; }
+// A operand of S^T for head-dim step dd from K stage `lds`.
+__device__ __forceinline__ u32x4 k_frag(const u16_t* lds, u32_t off) { return *(const u32x4*)((const char*)lds + off); }
 
-// A operand of S^T for head-dim step dd from K stage ST.
-template <int HD, int ST>
-__device__ __forceinline__ u32x4 k_frag(u32_t addr) {
-  u32x4 r;
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(ST * kStageBytes(HD)));
-  return r;
-}
-
-// A operand of O^T = V^T P^T for one head-dim tile (lane address addr) and 16-key step s from V
-// stage ST, keys in the permuted order: halves r = 0, 1 are rows 16 s + 8 r + ... of the tile.
-template <int HD, int ST, int S>
-__device__ __forceinline__ u32x4 v_frag(u32_t addr) {
-  u32x2 lo, hi;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo) : "v"(addr), "i"(ST * kStageBytes(HD) + 2 * (16 * S) * HD));
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(addr), "i"(ST * kStageBytes(HD) + 2 * (16 * S + 8) * HD));
-  return u32x4{lo[0], lo[1], hi[0], hi[1]};
-}
-
-// Waits until at most N of this wave's LDS reads are outstanding; the fragment passes through, so
-// the MFMA that reads it cannot move above the wait.
-template <int N>
-__device__ __forceinline__ void lgkm_wait_for(u32x4& frag) {
-  static_assert(N >= 0 && N < 16, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(frag) : "i"(N));
-}
-
-// The issue order of a step's fragment reads (a K fragment is one LDS instruction, a V fragment two):
-// PF K fragments (with HS) then PF V fragments (with HP) before the first MFMA; before MFMA event e,
-// the fragment PF events ahead of it in its own stream. Returns the lgkmcnt that completes the
-// fragment MFMA event e reads.
-template <bool HS, bool HP, int DS, int NPV, int PF>
-constexpr int lgkm_wait(int e) {
-  int issued = 0, end_k[32] = {}, end_v[32] = {};
-  if (HS)
-    for (int i = 0; i < PF && i < DS; ++i) end_k[i] = (issued += 1);
-  if (HP)
-    for (int i = 0; i < PF && i < NPV; ++i) end_v[i] = (issued += 2);
-  const int NE = (HS ? DS : 0) + (HP ? NPV : 0);
-  for (int ev = 0; ev < NE; ++ev) {
-    const bool is_s = HS && (!HP || (ev & 1) == 0);
-    const int i = HS && HP ? ev / 2 : ev;
-    int need;
-    if (is_s) {
-      if (i + PF < DS) end_k[i + PF] = (issued += 1);
-      need = end_k[i];
-    } else {
-      if (i + PF < NPV) end_v[i + PF] = (issued += 2);
-      need = end_v[i];
-    }
-    if (ev == e) return issued - need;
+// A operand of O^T = V^T P^T for one head-dim tile (offset off) and 16-key step s, keys in the
+// permuted order: halves r = 0, 1 are rows 16 s + 8 r + ... of the tile.
+template <int HD>
+__device__ __forceinline__ u32x4 v_frag(const u16_t* lds, u32_t off, int s) {
+  u32x4 out;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (ACCY_LDS i16x4*)((const char*)lds + off + 2 * (16 * s + 8 * r) * HD));
+    out[2 * r] = (u32_t)(u16_t)v[0] | ((u32_t)(u16_t)v[1] << 16);
+    out[2 * r + 1] = (u32_t)(u16_t)v[2] | ((u32_t)(u16_t)v[3] << 16);
   }
-  return 0;
+  return out;
 }
 
 // Probabilities P for the P.V product: an internal operand of the fused kernel (no traced value), packed
@@ -278,9 +230,8 @@ __device__ __forceinline__ float sum_with_partner(float x) {
 // clock drops as the work per cycle rises; every instruction removed from the loop counts.
 template <class C>
 struct Lds {
-  u16_t* const* ks;  // K stages [4][BK * HD], consecutive in one LDS array
-  u16_t* const* vs;  // V stages [4][BK * HD], consecutive in one LDS array
-  u32_t kbase, vbase;  // LDS addresses of stage 0
+  u16_t* const* ks;  // K stages [4][BK * HD]
+  u16_t* const* vs;  // V stages [4][BK * HD]
 };
 
 template <class C>
@@ -401,14 +352,16 @@ struct Worker {
     if constexpr (HM)
       if constexpr (C::CAUSAL) mask<PB>((t - 1) * BK);
 
+    const u16_t* kl = sh.ks[ST];
+    const u16_t* vl = sh.vs[VST];
     constexpr int PF = 2;  // fragments read ahead of their MFMA
     u32x4 kf[PF + 1], vf[PF + 1];
     if constexpr (HS) {
-      For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < DS) kf[i] = k_frag<HD, ST>(off.kf[i]); });
+      For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < DS) kf[i] = k_frag(kl, off.kf[i]); });
       s[SB] = f32x16{};
     }
     if constexpr (HP)
-      For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < NPV) vf[i] = v_frag<HD, VST, i % 2>(off.vf[i / 2]); });
+      For<0, PF>::run([&](auto ii) { constexpr int i = decltype(ii)::value; if constexpr (i < NPV) vf[i] = v_frag<HD>(vl, off.vf[i / 2], i % 2); });
     // The softmax of block t - 1: pair 0 while the first fragments arrive, pairs 1-7 between the
     // MFMAs, then the check of the lazy maximum.
     const float ml = -m;
@@ -421,15 +374,12 @@ struct Worker {
       // event e: score MFMA e / 2 and P.V MFMA e / 2 alternate when both are present
       constexpr bool is_s = HS && (!HP || (e & 1) == 0);
       constexpr int i = HS && HP ? e / 2 : e;
-      constexpr int W = lgkm_wait<HS, HP, DS, NPV, PF>(e);
       if constexpr (is_s) {
-        if constexpr (i + PF < DS) kf[(i + PF) % (PF + 1)] = k_frag<HD, ST>(off.kf[i + PF]);
-        lgkm_wait_for<W>(kf[i % (PF + 1)]);
+        if constexpr (i + PF < DS) kf[(i + PF) % (PF + 1)] = k_frag(kl, off.kf[i + PF]);
         s[SB] = gemm::mfma32x32x16<C::DT>(kf[i % (PF + 1)], qf[i], s[SB]);
       } else {
         // P.V MFMA i: head-dim tile i / 2, 16-key step i % 2
-        if constexpr (i + PF < NPV) vf[(i + PF) % (PF + 1)] = v_frag<HD, VST, (i + PF) % 2>(off.vf[(i + PF) / 2]);
-        lgkm_wait_for<W>(vf[i % (PF + 1)]);
+        if constexpr (i + PF < NPV) vf[(i + PF) % (PF + 1)] = v_frag<HD>(vl, off.vf[(i + PF) / 2], (i + PF) % 2);
         o[i / 2] = gemm::mfma32x32x16<C::DT>(vf[i % (PF + 1)], p[SB][i % 2], o[i / 2]);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -460,7 +410,7 @@ struct Worker {
                                       long nkc) {
     if (!ready) {
       load_q(qp, q0);
-      off.init(wave, lane, sh.kbase, sh.vbase);
+      off.init(wave, lane);
       dma_share<PER>(kb, 0, off.kg, sh.ks[0], wave);
       if (nkb > 1) dma_share<PER>(kb, BK * C::K_S, off.kg, sh.ks[1], wave);
     }
@@ -554,14 +504,14 @@ struct Worker {
     if (3 < nkb) dma_share<PER>(kb, 3 * BK * C::K_S, off.kg, sh.ks[3], wave);
     dma_share<PER>(vb, 0, off.vg, sh.vs[0], wave);
     if (1 < nkb) dma_share<PER>(vb, BK * C::V_S, off.vg, sh.vs[1], wave);
+    const u16_t* kl = sh.ks[0];
     u32x4 kf[3];
-    kf[0] = k_frag<HD, 0>(off.kf[0]);
-    kf[1] = k_frag<HD, 0>(off.kf[1]);
+    kf[0] = k_frag(kl, off.kf[0]);
+    kf[1] = k_frag(kl, off.kf[1]);
     s[0] = f32x16{};
     For<0, DS>::run([&](auto ii) {
       constexpr int i = decltype(ii)::value;
-      if constexpr (i + 2 < DS) kf[(i + 2) % 3] = k_frag<HD, 0>(off.kf[i + 2]);
-      lgkm_wait_for<lgkm_wait<true, false, DS, 0, 2>(i)>(kf[i % 3]);
+      if constexpr (i + 2 < DS) kf[(i + 2) % 3] = k_frag(kl, off.kf[i + 2]);
       s[0] = gemm::mfma32x32x16<C::DT>(kf[i % 3], qf[i], s[0]);
     });
   }
@@ -620,11 +570,10 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   constexpr long BQ = 32 * WAVES, NQB = C::SQ / BQ, PAIR = blocks_per_group<C>(), PER_B = NQB / PAIR;
   static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
   static_assert((HD == 64 || HD == 128 || HD == 256) && (HD / 16) % WAVES == 0, "head dimension 64, 128 or 256, whole load shares");
-  __shared__ __attribute__((aligned(1024))) u16_t kst[4 * BK * HD];
-  __shared__ __attribute__((aligned(1024))) u16_t vst[4 * BK * HD];
-  u16_t* const ks[4] = {kst, kst + BK * HD, kst + 2 * BK * HD, kst + 3 * BK * HD};
-  u16_t* const vs[4] = {vst, vst + BK * HD, vst + 2 * BK * HD, vst + 3 * BK * HD};
-  auto lds_addr = [](const u16_t* p) { return (u32_t)(unsigned long)(const ACCY_LDS u16_t*)p; };
+  __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
+  __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
+  u16_t* const ks[4] = {k0s, k1s, k2s, k3s};
+  u16_t* const vs[4] = {v0s, v1s, v2s, v3s};
 
   // Tiles of one batch index go to one XCD (they share K and V in its L2); under a causal mask the
   // query blocks with the most keys start first.
@@ -634,7 +583,7 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   const long b = t / PER_B, p = t % PER_B;
   if (b >= C::NB) return;  // a grid larger than the work
   Worker<C> f;
-  f.sh = Lds<C>{ks, vs, lds_addr(kst), lds_addr(vst)};
+  f.sh = Lds<C>{ks, vs};
   f.kb = K + C::k_off(b);
   f.vb = V + C::v_off(b);
   f.wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));

@@ -125,7 +125,8 @@ def exact_attention(q, k, v, scale, causal, dtype):
 def assert_rowwise(got, ref, tol, dtype, exact=None):
     """Parity of outputs built from long 16-bit op chains (attention, a decoder block). Against
     runCpu's per-op 16-bit evaluation: max|g-r| / max|r| <= tol over the whole output and over every
-    row (last axis). Against the float64 formula (when given): the error is at most 1.5x runCpu's own
+    row (last axis); where runCpu's own error is the larger (exact given), an output or row beyond tol
+    passes only if it is closer to the exact result than runCpu's. Against the float64 formula (when given): the error is at most 1.5x runCpu's own
     plus a 16-bit rounding of the largest output. (Where a result is a small difference of large
     16-bit intermediates, one rounding step of an intermediate moves it by more than a per-element
     relative bound allows, so none is asserted.)"""
@@ -136,7 +137,15 @@ def assert_rowwise(got, ref, tol, dtype, exact=None):
         return
     scale = np.abs(r).max()
     err = np.abs(g - r)
-    assert err.max() <= tol * scale, f"normwise error {err.max() / scale:.3e} > {tol}"
+    if exact is None or err.max() <= tol * scale:
+        assert err.max() <= tol * scale, f"normwise error {err.max() / scale:.3e} > {tol}"
+    else:
+        # runCpu's per-op 16-bit evaluation can itself be further than tol from the exact result (bf16
+        # attention rows over a few hundred keys: up to 2.9e-2 normwise); then the output passes only
+        # if it is no further from the exact result than runCpu's is.
+        mine, theirs = np.abs(g - exact).max(), np.abs(r - exact).max()
+        assert mine <= theirs, (f"normwise error {err.max() / scale:.3e} > {tol} and error vs exact {mine:.3e} "
+                                f"above runCpu's {theirs:.3e}")
     row_scale = np.abs(r).max(-1)
     row_err = err.max(-1)
     bad = row_err > tol * np.maximum(row_scale, 1e-30)

@@ -286,6 +286,29 @@ __device__ __forceinline__ void lds_reads_done_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// out[e] = the 16-bit LDS word at byte address addr[e], zero-extended: 16 reads and one wait in a
+// single assembly statement, so no result is visible to the compiler before its data has arrived
+// (split into one statement per read and one for the wait, a register copy or spill placed between
+// them would read the register early). Written as assembly because the lookups address LDS as a
+// whole: indexing the stage arrays makes the compiler branch on which array an index falls in, and
+// plain loads through an LDS pointer are each waited for before the next, since the epilogue's
+// stores go through generic pointers the compiler cannot separate from LDS.
+__device__ __forceinline__ void lds_gather16(const u32_t (&addr)[16], u32_t (&out)[16]) {
+  asm volatile(
+      "ds_read_u16 %0, %16\n ds_read_u16 %1, %17\n ds_read_u16 %2, %18\n ds_read_u16 %3, %19\n"
+      "ds_read_u16 %4, %20\n ds_read_u16 %5, %21\n ds_read_u16 %6, %22\n ds_read_u16 %7, %23\n"
+      "ds_read_u16 %8, %24\n ds_read_u16 %9, %25\n ds_read_u16 %10, %26\n ds_read_u16 %11, %27\n"
+      "ds_read_u16 %12, %28\n ds_read_u16 %13, %29\n ds_read_u16 %14, %30\n ds_read_u16 %15, %31\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]),
+        "=&v"(out[6]), "=&v"(out[7]), "=&v"(out[8]), "=&v"(out[9]), "=&v"(out[10]), "=&v"(out[11]),
+        "=&v"(out[12]), "=&v"(out[13]), "=&v"(out[14]), "=&v"(out[15])
+      : "v"(addr[0]), "v"(addr[1]), "v"(addr[2]), "v"(addr[3]), "v"(addr[4]), "v"(addr[5]), "v"(addr[6]),
+        "v"(addr[7]), "v"(addr[8]), "v"(addr[9]), "v"(addr[10]), "v"(addr[11]), "v"(addr[12]), "v"(addr[13]),
+        "v"(addr[14]), "v"(addr[15])
+      : "memory");
+}
+
 // Element offsets of an operand tile: O::row(i) of row (M or N) index i, O::k(i) of contraction
 // index i. The configuration struct supplies them as a_m / a_k / b_n / b_k (and a_b / b_b for the
 // batch index): plain products for strided operands, or sums over several axes when a named group
@@ -580,9 +603,8 @@ __device__ __forceinline__ void mma16_dma_tile(const u16_t* __restrict__ A, cons
     // A table epilogue (65536 16-bit results indexed by the rounded contraction value): with four
     // stages of 256 x 256 tiles the eight 16 KiB stage arrays are the kernel's whole 128 KiB of LDS,
     // i.e. they tile LDS addresses [0, 128 KiB) in some order. After the last K step each array
-    // receives the table entries of its own addresses, and the lookups read LDS address 2 x index
-    // (ds_read_u16 written as assembly, 16 per wait, since the compiler's view of the arrays ends
-    // at each one's bounds). Otherwise the table is read from global memory (L2).
+    // receives the table entries of its own addresses, and the lookups read LDS address 2 x index,
+    // 16 per wait (lds_gather16). Otherwise the table is read from global memory (L2).
     const u16_t* __restrict__ table = epi.table();
     bool in_lds = false;
     auto at = [](const u16_t* p) { return (u32_t)(unsigned long)(const ACCY_LDS u16_t*)p; };
@@ -611,16 +633,10 @@ __device__ __forceinline__ void mma16_dma_tile(const u16_t* __restrict__ A, cons
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          u32_t bits[16];
+          u32_t addr[16], bits[16];
 #pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const u32_t addr = 2u * (u32_t)Epi::index(acc[i][j][e]);
-            asm volatile("ds_read_u16 %0, %1" : "=v"(bits[e]) : "v"(addr));
-          }
-          asm volatile("s_waitcnt lgkmcnt(0)"
-                       : "+v"(bits[0]), "+v"(bits[1]), "+v"(bits[2]), "+v"(bits[3]), "+v"(bits[4]), "+v"(bits[5]),
-                         "+v"(bits[6]), "+v"(bits[7]), "+v"(bits[8]), "+v"(bits[9]), "+v"(bits[10]), "+v"(bits[11]),
-                         "+v"(bits[12]), "+v"(bits[13]), "+v"(bits[14]), "+v"(bits[15]));
+          for (int e = 0; e < 16; ++e) addr[e] = 2u * (u32_t)Epi::index(acc[i][j][e]);
+          lds_gather16(addr, bits);
 #pragma unroll
           for (int e = 0; e < 16; ++e) {
             const long m = row_base + i * 32 + (e >> 2) * 8 + (e & 3), n = col_base + j * 32;

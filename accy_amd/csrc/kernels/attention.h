@@ -1,6 +1,6 @@
 // Fused attention O[b, q, :] = softmax_k(scale * Q[b, q, :] . K[b, k, :] [masked k > q]) V[b, k, :] on
-// gfx950 matrix cores, for 16-bit Q, K, V with a head dimension HD of 64, 128 or 256 (both for Q.K and
-// for V), and (flash_f32, at the end) for f32 Q, K, V with a head dimension of 64.
+// gfx950 matrix cores, for 16-bit Q, K, V with a head dimension HD of 64 or 128 (both for Q.K and for
+// V), and (flash_f32, at the end) for f32 Q, K, V with a head dimension of 64.
 //
 // A workgroup of WAVES wavefronts owns 32 * WAVES queries of one batch index (32 per wave) and
 // streams the keys in blocks of 32; see the work split below.
@@ -64,15 +64,15 @@ constexpr int BK = 32;   // keys per block
 
 // LDS layouts of a K / V tile (32 key rows of HD 16-bit elements), conflict-free on the 64-bank LDS:
 //  * K: the 16-byte chunk c of key row r sits at chunk c ^ k_swizzle(r). A fragment's 16-lane group
-//    reads one chunk of 16 consecutive rows: with rows of 256 or 512 bytes (HD 128, 256) the XOR with
+//    reads one chunk of 16 consecutive rows: with rows of 256 bytes (HD 128) the XOR with
 //    r & 15 spreads them over the 16 positions of a 256-byte bank window; with 128-byte rows (HD 64)
 //    two rows share 256 bytes, and the XOR with (r / 2) & 7 spreads the 8 row pairs.
 //  * V: the 32-byte unit u of key row r sits at unit u ^ v_swizzle(r). A 32-lane half of a transposed
-//    read covers units (u, u ^ 1) of four consecutive rows: rows of 256 or 512 bytes use
+//    read covers units (u, u ^ 1) of four consecutive rows: 256-byte rows use
 //    gemm::tr_swizzle (2 (r & 3)); 128-byte rows (4 units, two rows per 256 bytes) XOR with
 //    2 ((r / 2) & 1).
-template <int HD> __device__ __forceinline__ int k_swizzle(int r) { return HD >= 128 ? (r & 15) : ((r >> 1) & 7); }
-template <int HD> __device__ __forceinline__ int v_swizzle(int r) { return HD >= 128 ? gemm::tr_swizzle(r) : 2 * ((r >> 1) & 1); }
+template <int HD> __device__ __forceinline__ int k_swizzle(int r) { return HD == 128 ? (r & 15) : ((r >> 1) & 7); }
+template <int HD> __device__ __forceinline__ int v_swizzle(int r) { return HD == 128 ? gemm::tr_swizzle(r) : 2 * ((r >> 1) & 1); }
 
 // Byte offsets, within a tile, of one lane's pieces of the K / V tiles, computed once per query
 // block. The per-step accesses then add only compile-time constants (LDS stage, key step) or a scalar
@@ -569,7 +569,7 @@ __device__ __forceinline__ void flash(const u16_t* __restrict__ Q, const u16_t* 
   constexpr int WAVES = C::WAVES, HD = C::HD;
   constexpr long BQ = 32 * WAVES, NQB = C::SQ / BQ, PAIR = blocks_per_group<C>(), PER_B = NQB / PAIR;
   static_assert(C::SQ % BQ == 0 && C::SK % BK == 0, "exact blocks only");
-  static_assert((HD == 64 || HD == 128 || HD == 256) && (HD / 16) % WAVES == 0, "head dimension 64, 128 or 256, whole load shares");
+  static_assert((HD == 64 || HD == 128) && (HD / 16) % WAVES == 0, "head dimension 64 or 128, whole load shares");
   __shared__ __attribute__((aligned(1024))) u16_t k0s[BK * HD], k1s[BK * HD], k2s[BK * HD], k3s[BK * HD];
   __shared__ __attribute__((aligned(1024))) u16_t v0s[BK * HD], v1s[BK * HD], v2s[BK * HD], v3s[BK * HD];
   u16_t* const ks[4] = {k0s, k1s, k2s, k3s};

@@ -50,36 +50,6 @@ extern "C" __global__ void __launch_bounds__(256) accy_check_attention_causal_bf
   accy::attn::flash<CheckAttnCausalBf16>(q, k, v, o);
 }
 
-struct CheckAttnHd256F16 {
-  static constexpr int DT = 1, HD = 256, WAVES = 4;
-  static constexpr long SQ = 1024, SK = 1024, NB = 4;
-  static constexpr long Q_S = 256, K_S = 256, V_S = 256;
-  static constexpr bool CAUSAL = false;
-  static constexpr float SL = 0x1.6a09e6p-3f;
-  static __device__ __forceinline__ long q_off(long b) { return b * 262144L; }
-  static __device__ __forceinline__ long k_off(long b) { return b * 262144L; }
-  static __device__ __forceinline__ long v_off(long b) { return b * 262144L; }
-};
-
-struct CheckAttnHd256CausalBf16 {
-  static constexpr int DT = 0, HD = 256, WAVES = 4;
-  static constexpr long SQ = 1024, SK = 1024, NB = 4;
-  static constexpr long Q_S = 256, K_S = 256, V_S = 256;
-  static constexpr bool CAUSAL = true;
-  static constexpr float SL = 0x1.6a09e6p-3f;
-  static __device__ __forceinline__ long q_off(long b) { return b * 262144L; }
-  static __device__ __forceinline__ long k_off(long b) { return b * 262144L; }
-  static __device__ __forceinline__ long v_off(long b) { return b * 262144L; }
-};
-
-extern "C" __global__ void __launch_bounds__(256) accy_check_attention_hd256_f16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
-  accy::attn::flash<CheckAttnHd256F16>(q, k, v, o);
-}
-
-extern "C" __global__ void __launch_bounds__(256) accy_check_attention_hd256_causal_bf16(const u16_t* q, const u16_t* k, const u16_t* v, u16_t* o) {
-  accy::attn::flash<CheckAttnHd256CausalBf16>(q, k, v, o);
-}
-
 struct CheckAttnF32Causal {
   static constexpr int WAVES = 4;
   static constexpr long SQ = 1024, SK = 1024, NB = 4;

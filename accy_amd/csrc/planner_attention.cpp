@@ -184,17 +184,30 @@ bool Planner::attention_layout(uint32_t pv, const Attn& at, AttnLayout& L) const
   const int vf = free_axis(vt.rank(), d.rhs_batch, d.rhs_contract);
   if (qf < 0 || kf < 0 || vf < 0 || d.rhs_contract.size() != 1) return false;
   const size_t qc = (size_t)qk.lhs_contract[0], kc = (size_t)qk.rhs_contract[0], vc = (size_t)d.rhs_contract[0];
-  // Head dimension (Q.K contraction and V's free axis, unit stride): 64, 128 or 256 for 16-bit
-  // operands (attn::flash), 64 for f32 (attn::flash_f32, the reference's flash pattern).
+  // Head dimension (Q.K contraction and V's free axis, unit stride): 64 or 128 for 16-bit operands
+  // (attn::flash), 64 for f32 (attn::flash_f32, the reference's flash pattern).
   const bool f32 = d.result.dtype == DType::f32;
   L.hd = qt.dims[qc].extent;
-  if (f32 ? L.hd != 64 : (L.hd != 64 && L.hd != 128 && L.hd != 256)) return false;
+  if (f32 ? L.hd != 64 : (L.hd != 64 && L.hd != 128)) return false;
   if (kt.dims[kc].extent != L.hd || vt.dims[(size_t)vf].extent != L.hd) return false;
   if (L.q.strides[qc] != 1 || L.k.strides[kc] != 1 || L.v.strides[(size_t)vf] != 1) return false;
   L.sq = qt.dims[(size_t)qf].extent;
   L.sk = kt.dims[(size_t)kf].extent;
   // 32 queries per wave and key blocks of 32 (both kernels)
   if (vt.dims[vc].extent != L.sk || L.sq % 32 != 0 || L.sk % 32 != 0 || L.sq == 0 || L.sk == 0) return false;
+  // Only shapes whose 16-bit kernel fits in 256 VGPRs without spilling fuse; the rest run unfused
+  // (score contraction, softmax row kernel, P.V contraction). Head dimension 128 keeps Q^T, O^T and
+  // two score tiles in 160 registers, which fits with multi-wave workgroups and one compiled loop
+  // tail: it needs queries in blocks of 64 (a one-wave workgroup issues every K / V load itself and
+  // keeps 16 load offsets), and under the causal mask query blocks and keys in multiples of 128, so
+  // that every block's key-block count is 0 (mod 4). Head dimension 256 (Q^T, O^T and the scores
+  // alone take 224 registers) always spilled. Spilling kernels are not only slow: the device
+  // compiler has crashed compiling one (in its pass that rewrites MFMAs around AGPR spill copies),
+  // taking the calling process with it. Head dimension 64 fits in every shape.
+  if (!f32 && L.hd == 128) {
+    if (L.sq % 64 != 0) return false;
+    if (at.causal && (L.sq % 128 != 0 || L.sk % 128 != 0)) return false;
+  }
   L.q_s = L.q.strides[(size_t)qf];
   L.k_s = L.k.strides[(size_t)kf];
   L.v_s = L.v.strides[vc];
@@ -239,11 +252,9 @@ void Planner::attention(uint32_t pv, const Attn& at, const AttnLayout& L) {
   int out = slots_.slot_of[pv] >= 0 ? slots_.slot_of[pv] : temp_slot(pv);
   // Waves per workgroup (32 queries each): eight (two per SIMD) when the queries divide, else the
   // largest count that does, with two or more workgroups per CU; every wave's share of a K / V tile
-  // (HD / 16 load instructions) must be whole. Head dimension 256 takes at most four (one wave per
-  // SIMD: its O and Q^T alone fill 192 registers, and its K / V stages 128 KiB of LDS).
+  // (HD / 16 load instructions) must be whole.
   int waves = 1;
   for (int w : {8, 4, 2}) {
-    if (L.hd == 256 && w > 4) continue;
     if (L.sq % (32 * w) == 0 && (L.hd / 16) % w == 0) {
       waves = w;
       break;

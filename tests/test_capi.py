@@ -56,9 +56,12 @@ def test_every_config_program_lowers_and_compiles_for_gfx950(name):
     (lambda: W.attention_program(2, 384, 128, "bf16", causal=True), True),
     (lambda: W.decoder_program(), True),
     (lambda: W.attention_program(2, 128, 64), True),      # head dimension 64 (16-bit)
-    (lambda: W.attention_program(2, 96, 128), True),      # 96 queries: one-wave workgroups
+    (lambda: W.attention_program(2, 96, 64), True),       # 96 queries: one-wave workgroups
+    (lambda: W.attention_program(2, 96, 128), False),     # one-wave workgroups at head dimension 128 spill
+    (lambda: W.attention_program(2, 192, 128), True),     # two-wave workgroups
+    (lambda: W.attention_program(2, 192, 128, "bf16", causal=True), False),  # causal: four loop tails spill
     (lambda: W.attention_program(2, 80, 128), False),     # 80 queries: not a multiple of 32
-    (lambda: W.attention_program(2, 256, 256), True),     # head dimension 256: one wave per SIMD
+    (lambda: W.attention_program(2, 256, 256), False),    # head dimension 256 spills: unfused kernels
     (lambda: W.attention_program(2, 128, 512), False),    # head dimension 512: unfused kernels
     (lambda: W.attention_program(2, 128, 64, "f32"), True),          # the reference's flash pattern
     (lambda: W.attention_program(1, 96, 64, "f32", causal=True), True),

@@ -198,15 +198,16 @@ def _scale(dtype):
 
 @pytest.mark.parametrize("heads,seq,dtype,causal", [
     (2, 256, "f16", False), (2, 256, "f16", True), (3, 384, "bf16", True), (1, 128, "bf16", False),
-    (2, 64, "f16", False), (1, 64, "f16", True),
-    # one-wave workgroups: a single key block (32 x 32), an odd number of causal query blocks
-    (1, 32, "f16", False), (2, 96, "bf16", True), (3, 160, "f16", False),
+    (2, 64, "f16", False), (3, 192, "bf16", False),
     # eight-wave causal blocks, paired per workgroup (waves 0-3 skip the key blocks above the diagonal)
-    (2, 512, "bf16", True), (1, 1024, "f16", True)])
+    (2, 512, "bf16", True), (1, 1024, "f16", True),
+    # unfused at head dimension 128 (the kernel would spill): one-wave workgroups (a single key block
+    # of 32 x 32, an odd number of causal query blocks), causal two-wave workgroups
+    (1, 32, "f16", False), (2, 96, "bf16", True), (3, 160, "f16", False), (1, 64, "f16", True)])
 def test_fused_attention_matches_oracle(heads, seq, dtype, causal):
     say(f"attention {heads} x {seq} x 128 {dtype} causal={causal}")
     prog = W.attention_program(heads, seq, 128, dtype, causal)
-    assert _fused(prog)
+    assert _fused(prog) == (seq % 64 == 0 and (not causal or seq % 128 == 0))
     ins = W.attention_inputs(heads, seq, 128, dtype, seed=seq + heads)
     exact = exact_attention(*ins, _scale(dtype), causal, dtype)
     assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype, exact)
@@ -232,19 +233,20 @@ def test_fused_bf16_attention_where_runcpu_is_off():
     assert_attention(got, ref, 2e-2, "bf16", exact)
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f16"])
-def test_fused_attention_head_dim_256_one_wave_causal(dtype):
-    """Head dimension 256 with 352 queries (11 blocks of 32: one-wave workgroups, the loop tail chosen
-    at run time) and 384 keys under the causal mask, three heads: a configuration whose kernel spills
-    registers, where fragment reads the compiler could not see (inline assembly with hand-placed LDS
-    waits, tried and dropped) let a spill copy a fragment before its data arrived. Against the oracle
-    and float64."""
-    say(f"attention {dtype} 3 x 352 queries x 384 keys x 256 causal")
-    specs = [T.spec(dtype, head=3, query=352, dim=256), T.spec(dtype, head=3, key=384, dim=256),
-             T.spec(dtype, head=3, key=384, dim=256)]
+@pytest.mark.parametrize("dtype,heads,sq,sk", [("bf16", 3, 352, 384), ("f16", 3, 224, 320)])
+def test_attention_head_dim_256_causal_runs_unfused(dtype, heads, sq, sk):
+    """Head dimension 256 under the causal mask with one-wave query blocks, where the fused kernel
+    spilled registers: 352 x 384 computed NaN with an earlier version of it (fragment reads the
+    compiler could not see, which a spill copied before their data arrived), and compiling 224 x 320
+    with three heads crashed the device compiler. Head dimension 256 now runs unfused. Against the
+    oracle and float64."""
+    say(f"attention {dtype} {heads} x {sq} queries x {sk} keys x 256 causal (unfused)")
+    specs = [T.spec(dtype, head=heads, query=sq, dim=256), T.spec(dtype, head=heads, key=sk, dim=256),
+             T.spec(dtype, head=heads, key=sk, dim=256)]
     prog = T.define("fa256", specs, W.attention_body(dtype, 256, True))
-    assert _fused(prog) and "WAVES = 1" in hip.plan_source(prog.encode(), compile=False)
-    ins = [W.to_dtype(W.normal(8000 + i, 3 * s * 256), dtype).reshape(3, s, 256) for i, s in enumerate((352, 384, 384))]
+    assert not _fused(prog)
+    ins = [W.to_dtype(W.normal(8000 + i, heads * s * 256), dtype).reshape(heads, s, 256)
+           for i, s in enumerate((sq, sk, sk))]
     scale = float(to_f32(W.to_dtype(np.array([1 / math.sqrt(256)]), dtype), dtype)[0])
     exact = exact_attention(*ins, scale, True, dtype)
     got = hip_run(prog, ins)[0]
@@ -278,11 +280,11 @@ def test_fused_causal_attention_more_queries_than_keys():
     assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, "bf16", exact)
 
 
-@pytest.mark.parametrize("heads,seq,hd,waves", [(256, 512, 128, 8), (128, 512, 256, 4)])
+@pytest.mark.parametrize("heads,seq,hd,waves", [(256, 512, 128, 8), (128, 512, 64, 4)])
 def test_fused_attention_paired_blocks_without_mask(heads, seq, hd, waves):
     """Without a mask, a workgroup takes two query blocks when the pairs fill whole rounds of 256
-    workgroups (256 heads x 2 blocks of 256 queries; 128 heads x 4 blocks of 128 queries at head
-    dimension 256); the first block issues the second's Q^T and first K tiles. Every head against
+    workgroups (256 heads x 2 blocks of 256 queries at head dimension 128; 128 heads x 4 blocks of 128
+    queries at 64); the first block issues the second's Q^T and first K tiles. Every head against
     float64, two heads against the oracle."""
     say(f"attention f16 {heads} x {seq} x {seq} x {hd} (paired blocks)")
     prog = W.attention_program(heads, seq, hd, "f16")
@@ -570,12 +572,13 @@ def test_fused_16bit_attention_head_dim_64(heads, seq, dtype, causal):
 
 
 @pytest.mark.parametrize("heads,seq,dtype,causal", [(2, 256, "f16", False), (2, 384, "bf16", True), (1, 96, "bf16", False),
-                                                    (2, 512, "bf16", True)])  # paired four-wave blocks
-def test_fused_16bit_attention_head_dim_256(heads, seq, dtype, causal):
-    """Head dimension 256: one wave per SIMD (four-wave workgroups, 128 KiB of K / V stages)."""
+                                                    (2, 512, "bf16", True)])
+def test_16bit_attention_head_dim_256(heads, seq, dtype, causal):
+    """Head dimension 256 runs unfused (its fused kernel would spill): score contraction, softmax row
+    kernel, P.V contraction."""
     say(f"{dtype} attention {heads} x {seq} x 256 causal={causal}")
     prog = W.attention_program(heads, seq, 256, dtype, causal=causal)
-    assert "accy::attn::flash<" in hip.plan_source(prog)
+    assert "accy::attn::flash<" not in hip.plan_source(prog)
     ins = W.attention_inputs(heads, seq, 256, dtype, seed=5 * heads + seq)
     scale = float(to_f32(W.to_dtype(np.array([1 / math.sqrt(256)]), dtype), dtype)[0])
     assert_attention(hip_run(prog, ins)[0], oracle_run(prog, ins)[0], 2e-2, dtype,

@@ -791,6 +791,13 @@ __device__ __forceinline__ void mma32f(const float* __restrict__ A, const float*
     lds_reads_done_barrier();
     step(a0, b0);
   }
+  // The accumulators stay in AGPRs through the K loop. (With an epilogue that computes on the values,
+  // the register allocator otherwise gave the loop's per-lane offsets to scratch memory and reloaded
+  // them every K step; a plain store takes its data from the AGPRs.)
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i][j]));
 
   const long col_base = n0 + wn * 128 + 4 * l32;
   const long row_base = m0 + wm * 128 + 4 * h;

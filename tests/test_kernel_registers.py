@@ -1,12 +1,19 @@
-"""The fused attention kernels fit in their registers in the shapes the planner fuses (CPU test).
+"""Generated matrix-core kernels fit in their registers (CPU test).
 
-A fused attention kernel that spills is slow, and compiling one has crashed the device compiler
-(a segmentation fault in its pass that rewrites MFMAs around AGPR spill copies), which ends the
-calling process. The planner therefore fuses only shapes whose kernel fits (planner_attention.cpp,
-attention_layout). These cases compile the planned attention kernel as the runtime does (the
-template text in place of its #include lines and the runtime's compiler options, offline hipcc
-here) and read the compiler's resource report: no scratch memory, and for the 16-bit kernel, whose
-MFMA results are forced into VGPRs, no AGPRs either (there they can only be spill slots).
+A kernel that spills registers to scratch memory is slow, and compiling a spilling kernel has crashed
+the device compiler (a segmentation fault in its pass that rewrites MFMAs around AGPR spill copies),
+which ends the calling process. So:
+
+* fused attention is planned only for shapes whose kernel fits (planner_attention.cpp,
+  attention_layout); the 16-bit kernel forces its MFMA results into VGPRs, so any AGPR it uses is a
+  spill slot;
+* the contraction kernels keep their accumulators in AGPRs and must not touch scratch, whatever
+  their epilogue (the f32 kernel spilled its K loop's offsets once its epilogue computed on the
+  values, before its accumulators were pinned to AGPRs after the loop).
+
+Each case compiles the planned kernel as the runtime does (the template text in place of its
+#include lines, the runtime's compiler options; offline hipcc here) and reads the compiler's resource
+report.
 """
 import math
 import re
@@ -63,17 +70,24 @@ UNFUSED = [
 ]
 
 
-def _attention_kernel(src: str) -> str:
-    """The planned attention kernel's source, with the template text in place of its #include lines
-    (as the runtime's full_kernel_source assembles it)."""
+def _kernels(src: str, marker: str):
+    """The planned kernels whose source contains marker, each with the template text in place of its
+    #include lines (as the runtime's full_kernel_source assembles it)."""
     parts = re.split(r"^// \S+ grid \d+ block \d+\n", src, flags=re.M)
-    found = [p for p in parts if "accy::attn::flash" in p]
+    out = []
+    for body in parts:
+        if marker not in body:
+            continue
+        for line, name in (('#include "gemm"\n', "gemm.h"), ('#include "attention"\n', "attention.h")):
+            body = body.replace(line, (KERNELS / name).read_text() + "\n", 1)
+        out.append((KERNELS / "common.h").read_text() + "\n" + body)
+    return out
+
+
+def _attention_kernel(src: str) -> str:
+    found = _kernels(src, "accy::attn::flash")
     assert len(found) == 1
-    body = found[0]
-    out = (KERNELS / "common.h").read_text() + "\n"
-    for line, name in (('#include "gemm"\n', "gemm.h"), ('#include "attention"\n', "attention.h")):
-        body = body.replace(line, (KERNELS / name).read_text() + "\n", 1)
-    return out + body
+    return found[0]
 
 
 def _resources(name: str, source: str, tmp: Path) -> dict:
@@ -113,3 +127,51 @@ def test_attention_shapes_that_would_spill_run_unfused(name, prog):
     # plans without the fused kernel and compiles (hiprtc, in this process)
     src = hip.plan_source(prog(), compile=True)
     assert "accy::attn::flash" not in src
+
+
+def _contraction(dtype, m, k, n, epi, ta=False):
+    sc = T.Type(dtype, ())
+    a_spec = T.spec(dtype, k=k, m=m) if ta else T.spec(dtype, m=m, k=k)
+    specs = [a_spec, T.spec(dtype, k=k, n=n), T.spec(dtype, m=m, n=n)]
+
+    def body(b, a):
+        x, w, r = a
+        d = x.contract(w, "k")
+        if epi == "scale":
+            d = d.mul(b.full_float(sc, 0.5))
+        elif epi == "gelu":
+            d = d.mul(b.full_float(sc, 0.5)).mul(d.mul(b.full_float(sc, 0.7978845608028654)).tanh().add(b.full_float(sc, 1.0)))
+        elif epi == "resid":
+            d = d.add(r)
+        elif epi == "tanh":
+            d = d.tanh()
+        return [d]
+    return T.define("mm", specs, body)
+
+
+CONTRACTIONS = [
+    ("c3 bf16 8192^3", lambda: W.gemm_program(8192, 8192, 8192, "bf16", "mulsum")),
+    ("c3 f32 8192^3", lambda: W.gemm_program(8192, 8192, 8192, "f32", "mulsum")),
+    ("c5 decoder block", lambda: W.decoder_program()),
+    ("f32 1024^2 x 256, scale", lambda: _contraction("f32", 1024, 256, 1024, "scale")),
+    ("f32 1184 x 256 x 768, residual", lambda: _contraction("f32", 1184, 256, 768, "resid")),
+    ("f32 512 x 224 x 1024, gelu", lambda: _contraction("f32", 512, 224, 1024, "gelu")),
+    ("f32 256 x 2048 x 272, tanh", lambda: _contraction("f32", 256, 2048, 272, "tanh")),
+    ("bf16 512^3, gelu table", lambda: _contraction("bf16", 512, 512, 512, "gelu")),
+    ("bf16 1024 x 32 x 1024, residual", lambda: _contraction("bf16", 1024, 32, 1024, "resid")),
+    ("f16 483 x 192 x 512, residual (register-staged)", lambda: _contraction("f16", 483, 192, 512, "resid")),
+    ("bf16 944 x 2048 x 256, scale", lambda: _contraction("bf16", 944, 2048, 256, "scale", ta=True)),
+]
+
+
+@pytest.mark.skipif(not HIPCC.exists(), reason="needs the ROCm compiler")
+def test_contraction_kernels_do_not_spill(tmp_path):
+    sources = []
+    for name, prog in CONTRACTIONS:
+        found = _kernels(hip.plan_source(prog(), compile=False), "accy::gemm::")
+        assert found, name
+        sources += [(f"{name} #{i}", src) for i, src in enumerate(found)]
+    with ThreadPoolExecutor(4) as ex:
+        results = list(ex.map(lambda c: (c[0], _resources(c[0], c[1], tmp_path)), sources))
+    bad = [f"{name}: {r}" for name, r in results if r["scratch"]]
+    assert not bad, "contraction kernels using scratch memory:\n" + "\n".join(bad)

@@ -73,9 +73,28 @@ int guarded(F&& f) {
   }
 }
 
+// The largest value (parameter, result or intermediate) a program may have: 1 TiB, more than one
+// device's HBM (288 GB), so such a program could never run; it is refused before planning with
+// OUT_OF_MEMORY, as an allocation would fail. The bound also keeps every product of extents the
+// planner forms (of at most three values' element counts) inside int64.
+constexpr uint64_t kMaxValueBytes = 1ull << 40;
+
+void check_capacity(const Graph& g) {
+  for (size_t i = 0; i < g.ops.size(); ++i) {
+    const Op& op = g.ops[i];
+    const uint64_t bytes = op.result.bytes();  // ShapeElementOverflow / ShapeByteOverflow past 2^64
+    if (bytes > kMaxValueBytes)
+      throw HipFailure(kStatusOutOfMemory, "value %" + std::to_string(i) + " needs " + std::to_string(bytes) +
+                                               " bytes, more than one device holds");
+    if (op.body) check_capacity(*op.body);
+  }
+}
+
 Program decode_program(const uint8_t* wire, size_t len) {
   if (!wire && len) throw Error(Err::InvalidArtifact, "null wire bytes");
-  return wire::decode(wire, len);
+  Program p = wire::decode(wire, len);
+  check_capacity(p);
+  return p;
 }
 
 void fill_descriptors(Entry& e) {

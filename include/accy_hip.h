@@ -30,7 +30,8 @@ enum {
   ACCY_HIP_INVALID_HANDLE = 3,
   ACCY_HIP_INVALID_BUFFER = 4,
   ACCY_HIP_TOO_MANY_PROGRAMS = 5,
-  ACCY_HIP_OUT_OF_MEMORY = 6,
+  ACCY_HIP_OUT_OF_MEMORY = 6,   /* also: a program with a value over 1 TiB (more than a device holds),
+                                   refused when it is decoded */
   ACCY_HIP_COMPILE_FAILED = 7,
   ACCY_HIP_LAUNCH_FAILED = 8
 };

@@ -144,6 +144,18 @@ def test_operands_sharing_one_buffer_compile():
     assert "accy::attn::flash" in hip.plan_source(self_attn, compile=True)
 
 
+def test_values_larger_than_a_device_holds_are_refused_before_planning():
+    # 2^20 x 2^19 f32 elements (2 TiB): OUT_OF_MEMORY from the decode step, as an allocation would
+    # fail, before the planner forms products of such extents
+    big = T.define("big", [T.spec("f32", m=1 << 20, n=1 << 19)], lambda b, a: [a[0].exp()])
+    with pytest.raises(hip.HipError) as e:
+        hip.plan_source(big)
+    assert e.value.status == 6 and "more than one device holds" in str(e.value)
+    # 1 TiB exactly is still planned
+    edge = T.define("edge", [T.spec("u8", m=1 << 20, n=1 << 20)], lambda b, a: [a[0].add(a[0])])
+    assert "__global__" in hip.plan_source(edge)
+
+
 def test_indexing_and_integer_programs_compile():
     def body(b, a):
         g = a[0].gather(a[1], "v")

@@ -73,27 +73,37 @@ int guarded(F&& f) {
   }
 }
 
-// The largest value (parameter, result or intermediate) a program may have: 1 TiB, more than one
-// device's HBM (288 GB), so such a program could never run; it is refused before planning with
-// OUT_OF_MEMORY, as an allocation would fail. The bound also keeps every product of extents the
-// planner forms (of at most three values' element counts) inside int64.
-constexpr uint64_t kMaxValueBytes = 1ull << 40;
+// Sizes this target plans. A parameter or output over 1 TiB (more than one device's 288 GB of HBM)
+// could never be allocated, and is refused when the program is decoded, with OUT_OF_MEMORY as an
+// allocation would fail. Intermediates may be larger as long as they are fused away (a contraction
+// spelled as a product and a sum has an [m, k, n] intermediate: 2 TiB of f32 at 8192^3), but no value
+// may exceed 2^50 elements: with that bound every product of extents within a value fits in int64.
+constexpr uint64_t kMaxMaterialBytes = 1ull << 40;
+constexpr uint64_t kMaxValueElements = 1ull << 50;
 
-void check_capacity(const Graph& g) {
+void check_capacity(const Graph& g, bool top) {
+  auto too_big = [](size_t i, const std::string& what) {
+    throw HipFailure(kStatusOutOfMemory, "value %" + std::to_string(i) + " " + what);
+  };
   for (size_t i = 0; i < g.ops.size(); ++i) {
     const Op& op = g.ops[i];
-    const uint64_t bytes = op.result.bytes();  // ShapeElementOverflow / ShapeByteOverflow past 2^64
-    if (bytes > kMaxValueBytes)
-      throw HipFailure(kStatusOutOfMemory, "value %" + std::to_string(i) + " needs " + std::to_string(bytes) +
-                                               " bytes, more than one device holds");
-    if (op.body) check_capacity(*op.body);
+    const uint64_t n = op.result.elements();  // ShapeElementOverflow past 2^64
+    if (n > kMaxValueElements) too_big(i, "has " + std::to_string(n) + " elements, more than this target plans");
+    if (op.body) check_capacity(*op.body, false);
+  }
+  if (!top) return;
+  std::vector<uint32_t> materialised = g.params;
+  materialised.insert(materialised.end(), g.outputs.begin(), g.outputs.end());
+  for (uint32_t id : materialised) {
+    const uint64_t bytes = g.type(id).bytes();
+    if (bytes > kMaxMaterialBytes) too_big(id, "needs " + std::to_string(bytes) + " bytes, more than one device holds");
   }
 }
 
 Program decode_program(const uint8_t* wire, size_t len) {
   if (!wire && len) throw Error(Err::InvalidArtifact, "null wire bytes");
   Program p = wire::decode(wire, len);
-  check_capacity(p);
+  check_capacity(p, true);
   return p;
 }
 

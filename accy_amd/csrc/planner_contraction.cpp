@@ -176,7 +176,7 @@ bool Planner::gemm_eligible(const Op& op, GemmShape& gs) const {
   DType d = op.result.dtype;
   if (d != DType::bf16 && d != DType::f16 && d != DType::f32) return false;
   if (!gemm_shape(op, gs)) return false;
-  if (gs.m * gs.n * gs.k == 0) return false;
+  if (gs.m == 0 || gs.n == 0 || gs.k == 0) return false;
   if (gs.batch > 65535) return false;  // the batch index is gridDim.y, at most 65535 on gfx950
   if (d == DType::f32) {
     // The f32 MFMA kernel: 256 x 256 x 32 tiles, A K-contiguous and B N-contiguous with 16-byte

@@ -145,15 +145,22 @@ def test_operands_sharing_one_buffer_compile():
 
 
 def test_values_larger_than_a_device_holds_are_refused_before_planning():
-    # 2^20 x 2^19 f32 elements (2 TiB): OUT_OF_MEMORY from the decode step, as an allocation would
-    # fail, before the planner forms products of such extents
+    # a 2^20 x 2^19 f32 parameter (2 TiB): OUT_OF_MEMORY when the program is decoded, as an
+    # allocation would fail
     big = T.define("big", [T.spec("f32", m=1 << 20, n=1 << 19)], lambda b, a: [a[0].exp()])
     with pytest.raises(hip.HipError) as e:
         hip.plan_source(big)
     assert e.value.status == 6 and "more than one device holds" in str(e.value)
-    # 1 TiB exactly is still planned
+    # 1 TiB exactly is planned
     edge = T.define("edge", [T.spec("u8", m=1 << 20, n=1 << 20)], lambda b, a: [a[0].add(a[0])])
     assert "__global__" in hip.plan_source(edge)
+    # an intermediate past 2^50 elements (a fused product of 2^17 x 2^17 x 2^17) is refused too
+    mm = W.gemm_program(1 << 17, 1 << 17, 1 << 17, "bf16", "mulsum")
+    with pytest.raises(hip.HipError) as e:
+        hip.plan_source(mm)
+    assert e.value.status == 6 and "more than this target plans" in str(e.value)
+    # the C3 spelling's 2 TiB intermediate (8192^3 f32) is fused away and planned
+    assert "mma32f" in hip.plan_source(W.gemm_program(8192, 8192, 8192, "f32", "mulsum"))
 
 
 def test_indexing_and_integer_programs_compile():

@@ -432,7 +432,16 @@ KernelStep Planner::gen_row(const RowShape& rs, const RowKernel& rk, bool commit
     Scope pre(body, "    ");
     std::string init = w.value(op.args[1], {}, pre);
     std::string acc = "acc" + std::to_string(j);
-    body << "    " << at << " " << acc << " = (" << at << ")" << init << ";\n";
+    // Every thread folds its share of the row, then the shares are combined. max / min may start
+    // every share from the init (it is idempotent under them); a sum takes the init once, in the
+    // first thread's share, and the others start from the additive identity (-0 for floats, so
+    // that a share of -0 elements stays -0).
+    if (r == Reducer::sum) {
+      const std::string zero = is_int(d) ? "(" + at + ")0" : (d == DType::f64 ? "-0.0" : "-0.0f");
+      body << "    " << at << " " << acc << " = " << tid << " == 0 ? (" << at << ")" << init << " : " << zero << ";\n";
+    } else {
+      body << "    " << at << " " << acc << " = (" << at << ")" << init << ";\n";
+    }
     std::ostringstream ib;
     Scope inner(ib, guard ? "          " : "        ");
     std::string x = w.value(op.args[0], full, inner);

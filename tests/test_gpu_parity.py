@@ -788,6 +788,43 @@ def test_16bit_arithmetic_chains_bit_exact(dtype):
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
 
 
+@pytest.mark.parametrize("dtype,rows,cols,axis", [
+    ("f32", 64, 5000, "c"),     # row kernel, a workgroup per row
+    ("i32", 4097, 1000, "c"),   # row kernel, a wave per row (four rows per workgroup)
+    ("bf16", 2050, 300, "c"),
+    ("i32", 4, 100000, "c"),    # row kernel, long rows
+    ("i32", 1 << 20, 4, "r"),   # chunked fold (few outputs over a long leading axis)
+    ("f32", 3, 64, "r"),        # serial fold over the leading axis
+    ("i32", 300, 64, "r")])
+def test_sum_with_an_init_takes_it_once(dtype, rows, cols, axis):
+    """A sum's init enters once per output. (The row kernel once started every thread's share of a
+    row from the init, adding it once per thread; found by running mutated programs against the
+    oracle.) A max with an init beside it in the same row kernel keeps its own. Against the oracle,
+    integers bit-exact."""
+    say(f"sum with init {dtype} {rows} x {cols} over {axis}")
+    init = 1000
+
+    def body(b, a):
+        if dtype == "i32":
+            c, lo = b.full(dtype, init), b.full(dtype, -5)
+        else:
+            c, lo = b.full_float(T.Type(dtype, ()), float(init)), b.full_float(T.Type(dtype, ()), -5.0)
+        return [a[0].reduce(c, "sum", axis), a[0].reduce(lo, "max", axis)]
+    prog = T.define("suminit", [T.spec(dtype, r=rows, c=cols)], body)
+    rng = np.random.default_rng(rows + cols)
+    if dtype == "i32":
+        x = rng.integers(-20, 20, size=(rows, cols)).astype(np.int32)
+    else:
+        x = W.to_dtype(rng.standard_normal((rows, cols)), dtype).reshape(rows, cols)
+    got, ref = hip_run(prog, [x]), oracle_run(prog, [x])
+    if dtype == "i32":
+        assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
+        assert np.array_equal(got[0], x.sum(axis=1 if axis == "c" else 0).astype(np.int32) + init)
+    else:
+        assert_rel(got[0], ref[0], 1e-5 if dtype == "f32" else 2e-2, dtype)
+        assert np.array_equal(got[1], ref[1])
+
+
 def test_bf16_serial_fold_truncates_at_the_store_bit_exact():
     """A bf16 sum over a leading axis runs as a serial fold in runCpu's order with an f32 accumulator;
     the stored value keeps the high half of the f32 (Bf16.fromF32, dtype.zig:6-9), bit for bit."""

@@ -664,3 +664,20 @@ def test_iota_broadcast_in_dim_transpose_and_select_against_numpy():
             assert sel[i, j] == (x[i, j] if x[i, j] < z[j, i] else -z[j, i])
     assert [int(v) for v in neg] == [_wrap(-int(v), "i32") for v in w]
     assert [int(v) for v in ab] == [_wrap(abs(int(v)), "i32") for v in w]
+
+
+@pytest.mark.parametrize("dtype", ["i32", "u64", "f32", "f64"])
+def test_sum_with_an_init_adds_it_once(dtype):
+    """reduce(x, init, sum) is init + x_0 + x_1 + ... (a fold from the init, reduction.zig:1140-1155):
+    the init enters once per output, whatever the reduced extent. Small integers keep the float sums
+    exact."""
+    npd = T.NUMPY_DTYPE[dtype]
+    x = (np.arange(6 * 50) % 13).astype(npd).reshape(6, 50)
+    init = 1000
+
+    def body(b, a):
+        c = b.full(dtype, init) if dtype[0] in "iu" else b.full_float(T.Type(dtype, ()), float(init))
+        return [a[0].reduce(c, "sum", "c"), a[0].reduce(c, "sum", "r")]
+    rows, cols = oracle_run(T.define("si", [T.spec(dtype, r=6, c=50)], body), [x])
+    assert np.array_equal(rows, (x.astype(np.float64).sum(axis=1) + init).astype(npd))
+    assert np.array_equal(cols, (x.astype(np.float64).sum(axis=0) + init).astype(npd))

@@ -13,6 +13,12 @@ Plan Planner::run() {
   needed_.assign(n, false);
   done_.assign(n, false);
   mark_live();
+  users_.assign(n, {});
+  for (uint32_t v = 0; v < n; ++v)
+    if (live_[v])
+      for (uint32_t a : g_.ops[v].args) users_[a].push_back(v);
+  is_output_.assign(n, false);
+  for (uint32_t o : g_.outputs) is_output_[o] = true;
   for (size_t i = 0; i < g_.params.size(); ++i) {
     uint32_t p = g_.params[i];
     const Type& t = g_.type(p);
@@ -90,6 +96,19 @@ void Planner::mark_live() {
     live_[v] = true;
     for (uint32_t a : g_.ops[v].args) stack.push_back(a);
   }
+}
+
+bool Planner::read_outside(uint32_t v, const std::set<uint32_t>& inside) const {
+  std::vector<uint32_t> stack = users_[v];
+  std::set<uint32_t> seen;
+  while (!stack.empty()) {
+    const uint32_t u = stack.back();
+    stack.pop_back();
+    if (inside.count(u) || !seen.insert(u).second) continue;
+    if (is_output_[u] || needed_[u] || !is_inlinable(g_.ops[u].kind)) return true;
+    stack.insert(stack.end(), users_[u].begin(), users_[u].end());
+  }
+  return false;
 }
 
 int Planner::temp_slot(uint32_t v) {

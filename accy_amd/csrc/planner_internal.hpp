@@ -207,6 +207,8 @@ class Planner {
   Plan plan_;
   Slots slots_;
   std::vector<bool> live_, needed_, done_;
+  std::vector<std::vector<uint32_t>> users_;  // live operations reading each value (top-level graph)
+  std::vector<bool> is_output_;
   int counter_ = 0;
   uint64_t max_elems_ = 1;
 
@@ -216,6 +218,10 @@ class Planner {
   void process(uint32_t v);
 
   void mark_live();
+  // True when some reader of v other than the operations in `inside` (one kernel's values) can need
+  // v from memory: an output, or a reader that is not elementwise, reached directly or through
+  // elementwise operations (which other kernels would evaluate again from their operands).
+  bool read_outside(uint32_t v, const std::set<uint32_t>& inside) const;
 
   int temp_slot(uint32_t v);
 

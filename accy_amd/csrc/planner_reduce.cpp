@@ -211,7 +211,14 @@ bool Planner::row_group(uint32_t r0) {
       if (!try_row(rs, rk)) rk.full_vals.pop_back();
     }
   }
-  for (uint32_t v : rk.reduces) temp_slot(v);
+  // A reduction whose value no other kernel reads stays in the kernel's registers (no slot, no
+  // store): C2's row maximum and sum, a norm's sum of squares. (Storing them cost 4.7 µs of C2's
+  // 163 µs in a standalone harness.)
+  std::set<uint32_t> inside(rk.reduces.begin(), rk.reduces.end());
+  inside.insert(rk.row_vals.begin(), rk.row_vals.end());
+  inside.insert(rk.full_vals.begin(), rk.full_vals.end());
+  for (uint32_t v : rk.reduces)
+    if (is_output_[v] || read_outside(v, inside)) temp_slot(v);
   for (uint32_t v : rk.row_vals) temp_slot(v);
   for (uint32_t v : rk.full_vals) temp_slot(v);
   KernelStep k = gen_row(rs, rk, true);
@@ -454,7 +461,8 @@ KernelStep Planner::gen_row(const RowShape& rs, const RowKernel& rk, bool commit
     red_var[j] = "red" + std::to_string(j);
     std::string res = is_int(d) ? "(" + std::string(compute_type(d)) + ")" + acc : round_to(d, acc);
     body << "    const " << compute_type(d) << " " << red_var[j] << " = " << res << ";\n";
-    if (commit) body << "    if (" << tid << " == 0) " << w.store(slots_.slot_of[rk.reduces[j]], "row", d, red_var[j]) << "\n";
+    if (commit && slots_.slot_of[rk.reduces[j]] >= 0)
+      body << "    if (" << tid << " == 0) " << w.store(slots_.slot_of[rk.reduces[j]], "row", d, red_var[j]) << "\n";
     avail = j + 1;
   }
   if (!rk.row_vals.empty()) {

@@ -521,6 +521,58 @@ struct DmaGroup {
 // contraction value) and put(batch, m, n, bits); others are called as epi(batch, m, n, v).
 template <class E, class = void> struct HasTable { static constexpr bool value = false; };
 template <class E> struct HasTable<E, decltype((void)E::kTable)> { static constexpr bool value = E::kTable; };
+// An epilogue with kStaged set reads other operands at the output's own row-major index and depends
+// on the contraction value only through its rounding to the 16-bit element type (every 16-bit
+// contraction result is rounded before any use). Its tile goes through LDS (staged_epilogue).
+template <class E, class = void> struct IsStaged { static constexpr bool value = false; };
+template <class E> struct IsStaged<E, decltype((void)E::kStaged)> { static constexpr bool value = E::kStaged; };
+
+// The 16-bit result of one output of a contraction of element type DT (0 bf16: the high half,
+// as every bf16 result; 1 f16: nearest even) and its value as f32.
+template <int DT> __device__ __forceinline__ u16_t result_bits(float v) { return DT == 0 ? f32_to_bf16(v) : f32_to_f16(v); }
+template <int DT> __device__ __forceinline__ float result_value(u16_t h) { return DT == 0 ? bf16_to_f32(h) : f16_to_f32(h); }
+
+// Epilogue of a 256 x 256 tile through LDS: the rounded 16-bit results are written to the eight
+// 16 KiB stage arrays (32 tile rows each, rows of 512 bytes whose 16-byte chunk c sits at
+// c ^ (row & 7), so that the two 32-lane halves of a write, four rows apart, and the 16-lane groups
+// of a row read hit distinct banks), then every thread takes 16-byte chunks of 8 consecutive
+// outputs of one row and calls the epilogue for them in column order. The operands the epilogue
+// reads and the output it writes are then accessed in whole row segments (512 bytes per 32 lanes)
+// instead of 2-byte pieces of 32 rows. acc[i][j][4 g + r] is output (row_base + 32 i + 8 g + r,
+// col_base + 32 j) of the wave; lo holds tile rows 0-127 (wm = 0), hi rows 128-255.
+template <class C, class Epi, int TM, int TN>
+__device__ __forceinline__ void staged_epilogue(const f32x16 (&acc)[TM][TN], u16_t* const (&lo)[4], u16_t* const (&hi)[4],
+                                                const Epi& epi, long batch, long m0, long n0, int tid, int lane, int wm,
+                                                int wn) {
+  static_assert(TM == 4 && TN == 4, "256 x 256 tiles of four waves");
+  wait_vmcnt<0>();
+  lds_reads_done_barrier();
+  const int hr = (lane >> 5) * 4, col = wn * 128 + (lane & 31);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    u16_t* const arr = wm ? hi[i] : lo[i];
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int rr = g * 8 + hr + r, c = col + j * 32;
+          arr[rr * 256 + (((c >> 3) ^ (rr & 7)) << 3) + (c & 7)] = result_bits<C::DT>(acc[i][j][g * 4 + r]);
+        }
+  }
+  lds_reads_done_barrier();
+  const int chunk = tid & 31;
+#pragma unroll
+  for (int it = 0; it < 32; ++it) {
+    const int row = it * 8 + (tid >> 5), rr = row & 31;
+    const u16_t* arr = it < 16 ? lo[it / 4] : hi[(it - 16) / 4];
+    const u32x4 w = *(const u32x4*)(arr + rr * 256 + ((chunk ^ (rr & 7)) << 3));
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      epi(batch, m0 + row, n0 + chunk * 8 + e, result_value<C::DT>((u16_t)(w[e >> 1] >> (16 * (e & 1)))));
+  }
+}
 
 // Requires K % 32 == 0 with at least STAGES K steps and 16-byte aligned rows (M or N not a multiple
 // of the tile: see dma_part);
@@ -599,7 +651,12 @@ __device__ __forceinline__ void mma16_dma_tile(const u16_t* __restrict__ A, cons
             if ((C::M % BM == 0 || m < C::M) && (C::N % BN == 0 || n < C::N)) f(m, n, acc[i][j][g * 4 + r]);
           }
   };
-  if constexpr (HasTable<Epi>::value) {
+  if constexpr (IsStaged<Epi>::value && !HasTable<Epi>::value && S == 4 && BM == 256 && BN == 256 &&
+                C::M % BM == 0 && C::N % BN == 0) {
+    u16_t* const lo[4] = {a0, a1, a2, a3};
+    u16_t* const hi[4] = {b0, b1, b2, b3};
+    staged_epilogue<C>(acc, lo, hi, epi, batch, m0, n0, tid, lane, wm, wn);
+  } else if constexpr (HasTable<Epi>::value) {
     // A table epilogue (65536 16-bit results indexed by the rounded contraction value): with four
     // stages of 256 x 256 tiles the eight 16 KiB stage arrays are the kernel's whole 128 KiB of LDS,
     // i.e. they tile LDS addresses [0, 128 KiB) in some order. After the last K step each array

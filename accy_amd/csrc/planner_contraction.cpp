@@ -1,6 +1,8 @@
 // Kernel formation for contractions on the matrix cores: operand layouts, f32 repacks, grouped
 // launches of one activation's projections, fused epilogues (lookup tables included) and the
 // elementwise mul + sum spelling.
+#include <algorithm>
+
 #include "planner_internal.hpp"
 
 namespace accy {
@@ -543,11 +545,18 @@ void Planner::gemm(uint32_t v, const GemmShape& gs, const OutStrides& os) {
       start = comma + 2;
     }
   }
+  // A 16-bit epilogue that reads buffers besides A, B and its output (a residual, a bias) goes
+  // through LDS in whole row segments (gemm.h staged_epilogue; measured on C5's MLP-down: 224 ->
+  // 219.7 us). A plain store does not (58.2 against 60.3 us staged for C5's q projection).
+  const std::string ps = w->params();
+  const long nparams = ps.empty() ? 0 : 1 + (long)std::count(ps.begin(), ps.end(), ',');
+  const bool staged = table_members.empty() && target != v && (d == DType::bf16 || d == DType::f16) && nparams > 3 &&
+                      !std::getenv("ACCY_GEMM_NO_STAGE");
   std::ostringstream src;
   KernelStep k;
   src << "#include \"gemm\"\n";
   src << "struct Epi_" << nm << " {\n" << members.str()
-      << table_members
+      << table_members << (staged ? "  static constexpr bool kStaged = true;\n" : "")
       << "  __device__ __forceinline__ void operator()(long b, long m, long n, float v) const {\n"
       << (target != v && table_members.empty() ? "    const float vv = " + round_to(d, "v") + ";\n" : "") << epi.str()
       << "  }\n};\n";

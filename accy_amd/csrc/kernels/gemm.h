@@ -727,7 +727,8 @@ __device__ __forceinline__ void mma16_dma(const u16_t* __restrict__ A, const u16
 // operand and output, in one launch of G x tiles workgroups (the projections of one activation:
 // one fill and drain of the machine instead of G). Consecutive indices of an XCD's range take the G
 // contractions of one tile, so the workgroups that read an A row panel run on the same XCD (its L2)
-// at about the same time. The epilogue functor takes the contraction index first: epi(g, b, m, n, v).
+// at about the same time. The epilogue functor gives contraction g's output (epi.out(g), chosen once
+// per workgroup) and stores into it: epi(out, b, m, n, v).
 template <class C, int G, class Epi>
 __device__ __forceinline__ void mma16_dma_group(const u16_t* __restrict__ A, const u16_t* const (&B)[G], const Epi& epi) {
   constexpr long TILES_M = (C::M + C::BM - 1) / C::BM, TILES_N = (C::N + C::BN - 1) / C::BN;
@@ -739,7 +740,8 @@ __device__ __forceinline__ void mma16_dma_group(const u16_t* __restrict__ A, con
 #pragma unroll
   for (int i = 1; i < G; ++i)
     if (g == i) Bg = B[i];
-  mma16_dma_tile<C>(A, Bg, [&](long b, long m, long n, float v) { epi(g, b, m, n, v); }, tm, tn);
+  u16_t* __restrict__ const out = epi.out(g);
+  mma16_dma_tile<C>(A, Bg, [&](long b, long m, long n, float v) { epi(out, b, m, n, v); }, tm, tn);
 }
 
 // ---------------------------------------------------------------------------------------------

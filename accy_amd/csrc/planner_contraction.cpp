@@ -279,9 +279,9 @@ bool Planner::gemm_siblings(uint32_t v, const GemmShape& gs, std::vector<std::pa
   const Op& op = g_.ops[v];
   const DType d = op.result.dtype;
   if (op.kind != Kind::dot_general || (d != DType::bf16 && d != DType::f16) || gs.multi) return false;
-  // Opt-in (ACCY_GEMM_GROUP): with the tile walk that reads the larger operand once per XCD, three
-  // separate launches of the decoder's projections measured faster (181 against 194 µs).
-  if (gs.m % 256 != 0 || gs.n % 256 != 0 || !std::getenv("ACCY_GEMM_GROUP")) return false;
+  // The decoder's three projections: 175.5 µs grouped against 186.6 µs in three launches (C5, one
+  // box). ACCY_GEMM_NO_GROUP plans separate launches.
+  if (gs.m % 256 != 0 || gs.n % 256 != 0 || std::getenv("ACCY_GEMM_NO_GROUP")) return false;
   int dm = 0, dn = 0;
   bool akc = gs.a_k == 1, bkc = gs.b_k == 1;
   if (!dma_eligible(gs, dm, dn, akc, bkc) || dm != 256 || dn != 256 || !plain_store(v)) return false;
@@ -323,7 +323,7 @@ void Planner::gemm_group(const std::vector<std::pair<uint32_t, GemmShape>>& grou
     const uint32_t u = group[i].first;
     bs.push_back(w.arg(group[i].second.b.slot, false) + " + " + std::to_string(group[i].second.b.offset) + "L");
     const int out = slots_.slot_of[u] >= 0 ? slots_.slot_of[u] : temp_slot(u);
-    cases << "      case " << i << ": " << w.store(out, cidx, d, "v") << " break;\n";
+    cases << "      case " << i << ": return " << w.arg(out, true) << ";\n";
     if (i) label += "&%" + std::to_string(u);
   }
   std::ostringstream members, inits;
@@ -343,8 +343,10 @@ void Planner::gemm_group(const std::vector<std::pair<uint32_t, GemmShape>>& grou
   std::ostringstream src;
   src << "#include \"gemm\"\n";
   src << "struct Epi_" << nm << " {\n" << members.str()
-      << "  __device__ __forceinline__ void operator()(int g, long b, long m, long n, float v) const {\n"
-      << "    switch (g) {\n" << cases.str() << "    }\n  }\n};\n";
+      << "  __device__ __forceinline__ u16_t* out(int g) const {\n"
+      << "    switch (g) {\n" << cases.str() << "      default: return nullptr;\n    }\n  }\n"
+      << "  __device__ __forceinline__ void operator()(u16_t* __restrict__ o, long b, long m, long n, float v) const {\n"
+      << "    accy::" << (d == DType::bf16 ? "st_bf16" : "st_f16") << "(o, " << cidx << ", v);\n  }\n};\n";
   src << "struct Cfg_" << nm << " {\n"
       << "  static constexpr int DT = " << (d == DType::bf16 ? 0 : 1) << ";\n"
       << "  static constexpr long M = " << gs.m << ", N = " << gs.n << ", K = " << gs.k << ";\n"

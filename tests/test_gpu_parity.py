@@ -318,21 +318,20 @@ def test_attention_full_size_on_sampled_heads():
 
 def test_grouped_projections_equal_separate_launches():
     """Contractions of one activation with the same extents and layouts (a decoder block's q, k and v
-    projections) run as one grouped launch when ACCY_GEMM_GROUP is set (separate launches otherwise);
-    each output keeps its own k order, so the results equal separate launches bit for bit, and match
-    the oracle."""
+    projections) run as one grouped launch (separate launches with ACCY_GEMM_NO_GROUP); each output
+    keeps its own k order, so the results equal separate launches bit for bit, and match the oracle."""
     import os
     prog = W.decoder_program(1, 256, 512, 4, 128, 1024)
-    assert "mma16_dma_group" not in hip.plan_source(prog.encode(), compile=False)
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "mma16_dma_group" in src and "&%" in src
     ins = W.decoder_inputs(1, 256, 512, 4, 128, 1024, seed=12)
-    separate = hip_run(prog, ins)[0]
-    os.environ["ACCY_GEMM_GROUP"] = "1"
+    grouped = hip_run(prog, ins)[0]
+    os.environ["ACCY_GEMM_NO_GROUP"] = "1"
     try:
-        src = hip.plan_source(prog.encode(), compile=False)
-        assert "mma16_dma_group" in src and "&%" in src
-        grouped = hip_run(prog, ins)[0]
+        assert "mma16_dma_group" not in hip.plan_source(prog.encode(), compile=False)
+        separate = hip_run(prog, ins)[0]
     finally:
-        del os.environ["ACCY_GEMM_GROUP"]
+        del os.environ["ACCY_GEMM_NO_GROUP"]
     assert np.array_equal(grouped, separate)
     assert_rowwise(grouped, oracle_run(prog, ins)[0], 2e-2, "bf16")
 

@@ -384,38 +384,44 @@ def test_epilogue_lookup_table_equals_direct_epilogue(dtype, shape):
     assert_rowwise(table, oracle_run(prog, ins)[0], 2e-2, dtype)
 
 
-def _residual_contraction(dtype, batch, m, k, n):
-    """R[b, m, n] + (A[b, m, k] . B[k, n]) * 0.5 - R[b, m, n] * R[b, m, n]: a 16-bit contraction whose
-    fused epilogue reads another operand at the output's index (a residual)."""
-    specs = [T.spec(dtype, b=batch, m=m, k=k), T.spec(dtype, k=k, n=n), T.spec(dtype, b=batch, m=m, n=n)]
+def _residual_contraction(dtype, batch, m, k, n, batched_b=False, bias=False):
+    """(A[b, m, k] . B[k, n]) * 0.5 + R[b, m, n] - R[b, m, n] * R[b, m, n]: a 16-bit contraction whose
+    fused epilogue reads another operand at the output's index (a residual). batched_b gives B its own
+    batch axis (a batched contraction); bias makes R a vector over n, broadcast over b and m."""
+    bspec = T.spec(dtype, b=batch, k=k, n=n) if batched_b else T.spec(dtype, k=k, n=n)
+    rspec = T.spec(dtype, n=n) if bias else T.spec(dtype, b=batch, m=m, n=n)
+    specs = [T.spec(dtype, b=batch, m=m, k=k), bspec, rspec]
     scalar = T.Type(dtype, ())
 
     def body(bb, a):
         x = a[0].contract(a[1], "k")
         r = a[2]
-        return [r.add(x.mul(bb.full_float(scalar, 0.5))).sub(r.mul(r))]
+        return [x.mul(bb.full_float(scalar, 0.5)).add(r).sub(r.mul(r))]
 
     return T.define("residual_" + dtype, specs, body)
 
 
-@pytest.mark.parametrize("dtype,shape", [
-    ("bf16", (1, 512, 256, 768)), ("f16", (2, 256, 512, 512)),
+@pytest.mark.parametrize("dtype,shape,batched_b,bias", [
+    ("bf16", (1, 512, 256, 768), False, False), ("f16", (2, 256, 512, 512), False, False),
+    ("bf16", (3, 256, 256, 512), True, False), ("bf16", (2, 512, 256, 256), False, True),
     # not a multiple of the 256 x 256 tile: the direct epilogue
-    ("bf16", (1, 320, 256, 384))])
-def test_staged_epilogue_equals_direct_epilogue(dtype, shape):
+    ("bf16", (1, 320, 256, 384), False, False)])
+def test_staged_epilogue_equals_direct_epilogue(dtype, shape, batched_b, bias):
     """A 16-bit contraction whose fused epilogue reads another operand (a residual) stages its rounded
     tile through LDS and runs the epilogue on 16-byte row chunks (gemm.h staged_epilogue) when the
     tile is 256 x 256 with four stages. The outputs equal the per-element epilogue
     (ACCY_GEMM_NO_STAGE) bit for bit, and match the oracle."""
     import os
     batch, m, k, n = shape
-    say(f"staged epilogue {dtype} {batch} x {m} x {k} x {n}")
-    prog = _residual_contraction(dtype, batch, m, k, n)
+    say(f"staged epilogue {dtype} {batch} x {m} x {k} x {n} batched_b={batched_b} bias={bias}")
+    prog = _residual_contraction(dtype, batch, m, k, n, batched_b, bias)
     src = hip.plan_source(prog.encode(), compile=False)
     assert "kStaged = true" in src
     rng = np.random.default_rng(41)
-    ins = [W.to_dtype(rng.standard_normal((batch, m, k)), dtype), W.to_dtype(rng.standard_normal((k, n)) / 8, dtype),
-           W.to_dtype(rng.standard_normal((batch, m, n)), dtype)]
+    bshape = (batch, k, n) if batched_b else (k, n)
+    rshape = (n,) if bias else (batch, m, n)
+    ins = [W.to_dtype(rng.standard_normal((batch, m, k)), dtype), W.to_dtype(rng.standard_normal(bshape) / 8, dtype),
+           W.to_dtype(rng.standard_normal(rshape), dtype)]
     staged = hip_run(prog, ins)[0]
     os.environ["ACCY_GEMM_NO_STAGE"] = "1"
     try:

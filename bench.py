@@ -30,7 +30,9 @@ import json
 import math
 import os
 import re
+import subprocess
 import sys
+import threading
 import time
 from pathlib import Path
 
@@ -259,7 +261,44 @@ def oracle_time(name: str, cfg, budget_s: float):
                                  sample=f"median of {n_one} runs, {t_one:.3f} s each"))
 
 
-def measure(name: str, cfg: dict, steps: int, warmup: int, warmup_s: float) -> dict:
+def board_sample():
+    """Board power (W) and the mean graphics clock (MHz) over the XCDs from amd-smi, or None."""
+    try:
+        r = subprocess.run(["amd-smi", "metric", "-p", "-c", "--json"], capture_output=True, text=True, timeout=30)
+        d = json.loads(r.stdout)
+        g = d["gpu_data"][0] if isinstance(d, dict) else d[0]
+        clocks = [v["clk"]["value"] for k, v in g["clock"].items() if k.startswith("gfx_") and isinstance(v, dict)]
+        return dict(power_w=float(g["power"]["socket_power"]["value"]), gfx_mhz=sum(clocks) / len(clocks))
+    except Exception:  # no amd-smi, or a format it does not give here
+        return None
+
+
+def power_leg(step, stream, seconds: float = 1.2):
+    """Board power and clock under the config's sustained back-to-back steps (after the timed and
+    profiled steps, outside both): steps run in ~20 ms chunks for `seconds` while a thread samples
+    amd-smi once, past the first half."""
+    out = {}
+    t0 = time.perf_counter()
+
+    def sampler():
+        time.sleep(seconds / 2)
+        out["sample"] = board_sample()
+
+    th = threading.Thread(target=sampler)
+    th.start()
+    while time.perf_counter() - t0 < seconds or th.is_alive():
+        t = time.perf_counter()
+        step()
+        stream.synchronize()
+        n = max(1, int(0.02 / max(time.perf_counter() - t, 1e-6)))
+        for _ in range(n):
+            step()
+        stream.synchronize()
+    th.join()
+    return out.get("sample")
+
+
+def measure(name: str, cfg: dict, steps: int, warmup: int, warmup_s: float, power: bool = False) -> dict:
     """Runs one config on the GPU: K timed steps over HBM-resident inputs, then K profiled steps for
     the per-kernel durations. Returns the step time, the throughput and the dominant kernel's
     roofline entry."""
@@ -327,6 +366,7 @@ def measure(name: str, cfg: dict, steps: int, warmup: int, warmup_s: float) -> d
         peak = cfg["peak"] / 1000.0 if cfg["unit"] == "GFLOP/s" else cfg["peak"]
         roof = dict(bound=cfg["bound"], achieved=achieved, peak=peak, unit="TFLOP/s", frac=achieved / peak,
                     traffic=measured_traffic(name, dominant[0]), kernel=dominant[0], kernel_ms=dom_ms)
+    board = power_leg(step, stream) if power else None
     insts = measured_valu(name, dominant[0])
     if insts is not None:
         # VALU issue fraction (instructions x 64 lanes per second against 256 CUs x 2.4 GHz x 64)
@@ -335,9 +375,12 @@ def measure(name: str, cfg: dict, steps: int, warmup: int, warmup_s: float) -> d
     for b in dins + douts:
         b.free()
     stream.destroy()
-    return dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"], warmup_run=done,
-                workload=dict(workload=name, **cfg["workload"]), roofline=roof,
-                kernels={lbl: float(k.mean_ms) for lbl, k in per_kernel.items()})
+    r = dict(value=value, unit=cfg["unit"], ms_per_step=ms_per_step, dtype=cfg["dtype"], warmup_run=done,
+             workload=dict(workload=name, **cfg["workload"]), roofline=roof,
+             kernels={lbl: float(k.mean_ms) for lbl, k in per_kernel.items()})
+    if power:
+        r["board"] = board
+    return r
 
 
 HEADLINE = "c2-lse"
@@ -359,6 +402,8 @@ def main() -> int:
     ap.add_argument("--config", default="all",
                     help="'all' (the headline C2 line plus every config under 'configs') or one config")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--power", action="store_true",
+                    help="after each config's timed steps, sample board power and clock (amd-smi) under sustained steps")
     ap.add_argument("--cpu-budget", type=float, default=6.0,
                     help="seconds per CPU leg for the headline config (the other configs get a third)")
     args = ap.parse_args()
@@ -372,7 +417,7 @@ def main() -> int:
     results = {}
     for name in names:
         print(f"bench: {name}", file=sys.stderr, flush=True)
-        r = measure(name, cfgs[name], args.steps, args.warmup, args.warmup_seconds)
+        r = measure(name, cfgs[name], args.steps, args.warmup, args.warmup_seconds, args.power)
         budget = args.cpu_budget if name == head else args.cpu_budget / 3
         r["cpu_baseline"] = None if args.no_cpu else oracle_time(name, cfgs[name], budget)
         results[name] = r
@@ -385,6 +430,8 @@ def main() -> int:
         "config": h["workload"], "roofline": h["roofline"], "cpu_baseline": h["cpu_baseline"],
         "kernels": h["kernels"],
     }
+    if args.power:
+        line["board"] = h["board"]
     if len(names) > 1:
         line["configs"] = {
             n: dict(ms=r["ms_per_step"], value=r["value"], unit=r["unit"], dtype=r["dtype"], warmup_steps_run=r["warmup_run"],
@@ -393,7 +440,7 @@ def main() -> int:
                     achieved=r["roofline"]["achieved"], peak=r["roofline"]["peak"],
                     roofline_unit=r["roofline"]["unit"], frac=r["roofline"]["frac"],
                     traffic=r["roofline"]["traffic"], valu_issue=r["roofline"].get("valu_issue"),
-                    cpu_baseline=r["cpu_baseline"], kernels=r["kernels"])
+                    cpu_baseline=r["cpu_baseline"], kernels=r["kernels"], **({"board": r["board"]} if args.power else {}))
             for n, r in results.items()}
     print(json.dumps(line), flush=True)
     return 0

@@ -316,6 +316,40 @@ def test_attention_full_size_on_sampled_heads():
     assert_attention(got[heads], ref, 2e-2, "f16", exact_attention(*sub, _scale("f16"), False, "f16"))
 
 
+def _shared_activation_contractions(dtype, g, m=512, k=256, n=256):
+    """G contractions of one activation X[m, k] with weights W_i[k, n], returned as G outputs."""
+    specs = [T.spec(dtype, m=m, k=k)] + [T.spec(dtype, k=k, n=n) for _ in range(g)]
+
+    def body(b, a):
+        return [a[0].contract(w, "k") for w in a[1:]]
+
+    return T.define(f"shared_{dtype}_{g}", specs, body)
+
+
+@pytest.mark.parametrize("dtype,g", [("bf16", 2), ("f16", 3), ("bf16", 4)])
+def test_grouped_contractions_of_one_activation(dtype, g):
+    """Two, three and four contractions of one activation run as one grouped launch; every output
+    equals its separate launch (ACCY_GEMM_NO_GROUP) bit for bit and matches the oracle."""
+    import os
+    prog = _shared_activation_contractions(dtype, g)
+    src = hip.plan_source(prog.encode(), compile=False)
+    assert "mma16_dma_group" in src and src.count("&%") == g - 1
+    rng = np.random.default_rng(60 + g)
+    ins = [W.to_dtype(rng.standard_normal((512, 256)), dtype)] + \
+          [W.to_dtype(rng.standard_normal((256, 256)) / 8, dtype) for _ in range(g)]
+    grouped = hip_run(prog, ins)
+    os.environ["ACCY_GEMM_NO_GROUP"] = "1"
+    try:
+        assert "mma16_dma_group" not in hip.plan_source(prog.encode(), compile=False)
+        separate = hip_run(prog, ins)
+    finally:
+        del os.environ["ACCY_GEMM_NO_GROUP"]
+    ref = oracle_run(prog, ins)
+    for i in range(g):
+        assert np.array_equal(np.asarray(grouped[i]).view(np.uint8), np.asarray(separate[i]).view(np.uint8))
+        assert_normwise(grouped[i], ref[i], 2e-2, dtype)
+
+
 def test_grouped_projections_equal_separate_launches():
     """Contractions of one activation with the same extents and layouts (a decoder block's q, k and v
     projections) run as one grouped launch (separate launches with ACCY_GEMM_NO_GROUP); each output
